@@ -1,0 +1,91 @@
+/*
+ * libmoegemm: MI355X (gfx950) grouped and single GEMM kernels behind a plain C ABI.
+ *
+ * This is the native boundary of the MoE expert-GEMM hot path.  The Python layer
+ * (kernels/grouped_gemm.py and kernels/matmul.py of this project) keeps the reference's Python
+ * signatures and calls these functions through ctypes; any other host language binds the same
+ * symbols.  Conventions:
+ *   - all matrix, table and stream arguments are plain device pointers / a hipStream_t as void*;
+ *   - strides are in elements; dims tables are int32 (m, n, k) triples; pointer tables are int64
+ *     device addresses, read by the kernel at run time (callers may rewrite them between calls);
+ *   - a call performs exactly one kernel launch on `stream` (or none for an empty problem set),
+ *     never allocates, copies or synchronizes, and is therefore capturable in a HIP graph;
+ *   - the return value is MOEGEMM_OK or a negative error code; moegemm_last_error() returns the
+ *     message of the most recent failure on the calling thread.
+ */
+#ifndef MOEGEMM_H
+#define MOEGEMM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOEGEMM_ABI_VERSION 1
+
+#define MOEGEMM_OK 0
+#define MOEGEMM_ERR_INVALID (-1)   /* bad shape, pointer, dtype or parameter (Python: ValueError) */
+#define MOEGEMM_ERR_NO_KERNEL (-2) /* no compiled instantiation for the tile config (RuntimeError) */
+#define MOEGEMM_ERR_LAUNCH (-3)    /* the HIP runtime rejected the launch (RuntimeError) */
+
+#define MOEGEMM_DTYPE_F16 0
+#define MOEGEMM_DTYPE_BF16 1
+#define MOEGEMM_DTYPE_F32 2
+
+#define MOEGEMM_PRECISION_IEEE 0 /* operands used as given */
+#define MOEGEMM_PRECISION_TF32 1 /* fp32 operands rounded to a 10-bit mantissa (ties away) */
+
+/* ABI version of the loaded library (MOEGEMM_ABI_VERSION when header and library agree). */
+int moegemm_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* moegemm_last_error(void);
+
+/*
+ * Compiled tile configurations.  Replaces the Triton config pools
+ * (reference kernels/matmul.py:95-139 _MATMUL_CONFIG_POOL and kernels/grouped_gemm.py:41-64
+ * _GROUPED_EXTRA_CONFIG_POOL): the Python candidate generators enumerate this table instead.
+ * moegemm_kernel_info fills out7 = {block_m, block_n, block_k, num_warps (wave64 per
+ * workgroup), num_stages (LDS stages), lds_bytes, waves_m}.
+ */
+int moegemm_kernel_count(int dtype);
+int moegemm_kernel_info(int dtype, int index, int32_t* out7);
+
+/*
+ * Persistent grouped GEMM: for each problem e, C_e[m, n] = sum_k A_e[m, k] * B_e[k, n] with fp32
+ * accumulation, stored in the operand dtype.  Replaces the two Triton kernels launched by
+ * reference kernels/grouped_gemm.py:618-760 (launch_grouped):
+ *   homogeneous != 0 -> _homogeneous_grouped_kernel_impl (kernels/grouped_gemm.py:321-397):
+ *       every problem is (m, k) @ (k, n), all row-major contiguous; dims/strides may be NULL.
+ *   homogeneous == 0 -> _generic_grouped_kernel_impl (kernels/grouped_gemm.py:399-482):
+ *       per-problem dims [G,3] = (m, n, k) and strides [G,6] = (am, ak, bk, bn, cm, cn), the
+ *       tables built at kernels/grouped_gemm.py:536-544; total_tiles = sum over problems of
+ *       ceil(m/block_m) * ceil(n/block_n); m, n, k are ignored.
+ * group_size_m is the GROUP_M traversal width inside each problem; grid_size is the persistent
+ * grid (reference _grid_size, kernels/grouped_gemm.py:597-599); <= 0 means one workgroup per tile.
+ */
+int moegemm_grouped_gemm(const int64_t* a_ptrs, const int64_t* b_ptrs, const int64_t* c_ptrs,
+                         const int32_t* dims, const int64_t* strides, int32_t problem_count,
+                         int32_t m, int32_t n, int32_t k, int32_t homogeneous, int32_t total_tiles,
+                         int32_t dtype, int32_t input_precision, int32_t block_m, int32_t block_n,
+                         int32_t block_k, int32_t group_size_m, int32_t num_warps,
+                         int32_t num_stages, int32_t grid_size, void* stream);
+
+/*
+ * Masked single GEMM with arbitrary strides, C = A @ B.  Replaces the Triton launch of
+ * reference kernels/matmul.py:373-433 (launch_matmul -> _matmul_kernel_impl, :264-314); shape
+ * and dtype validation (kernels/matmul.py:359-370) stays in Python.  grid_size <= 0 launches one
+ * workgroup per output tile like the reference's 1-D grid; a positive value makes it persistent.
+ */
+int moegemm_matmul(const void* a, const void* b, void* c, int32_t m, int32_t n, int32_t k,
+                   int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
+                   int64_t stride_cm, int64_t stride_cn, int32_t dtype, int32_t input_precision,
+                   int32_t block_m, int32_t block_n, int32_t block_k, int32_t group_size_m,
+                   int32_t num_warps, int32_t num_stages, int32_t grid_size, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOEGEMM_H */

@@ -1,0 +1,183 @@
+// C ABI of libmoegemm: the native boundary under kernels/grouped_gemm.py and kernels/matmul.py.
+//
+// Every entry point takes plain device pointers, integer sizes and a hipStream_t passed as void*.
+// Nothing here allocates, synchronizes or copies: a call is one kernel launch on the caller's
+// stream (capturable in a HIP graph) or an error code with a message in moegemm_last_error().
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/moegemm.h"
+#include "registry.h"
+
+using namespace moegemm;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+const KernelEntry* table_for(int dtype, int* count) {
+  switch (dtype) {
+    case DT_BF16: *count = kNumBf16; return kEntriesBf16;
+    case DT_F16: *count = kNumF16; return kEntriesF16;
+    case DT_F32: *count = kNumF32; return kEntriesF32;
+    default: *count = 0; return nullptr;
+  }
+}
+
+const KernelEntry* find_entry(int dtype, int bm, int bn, int bk, int warps, int stages) {
+  int count = 0;
+  const KernelEntry* t = table_for(dtype, &count);
+  for (int i = 0; i < count; ++i) {
+    const KernelEntry& e = t[i];
+    if (e.block_m == bm && e.block_n == bn && e.block_k == bk && e.num_warps == warps && e.num_stages == stages)
+      return &e;
+  }
+  return nullptr;
+}
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+int check_common(int dtype, int input_precision, int group_size_m, const KernelEntry** entry, int bm, int bn, int bk,
+                 int warps, int stages) {
+  if (dtype != DT_F16 && dtype != DT_BF16 && dtype != DT_F32)
+    return fail(MOEGEMM_ERR_INVALID, "unsupported dtype code %d", dtype);
+  if (input_precision != MOEGEMM_PRECISION_IEEE && input_precision != MOEGEMM_PRECISION_TF32)
+    return fail(MOEGEMM_ERR_INVALID, "unsupported input precision code %d", input_precision);
+  if (input_precision == MOEGEMM_PRECISION_TF32 && dtype != DT_F32)
+    return fail(MOEGEMM_ERR_INVALID, "tf32 input precision requires fp32 operands");
+  if (group_size_m <= 0) return fail(MOEGEMM_ERR_INVALID, "group_size_m must be positive (got %d)", group_size_m);
+  *entry = find_entry(dtype, bm, bn, bk, warps, stages);
+  if (!*entry)
+    return fail(MOEGEMM_ERR_NO_KERNEL,
+                "no compiled kernel for dtype=%d block_m=%d block_n=%d block_k=%d num_warps=%d num_stages=%d", dtype, bm,
+                bn, bk, warps, stages);
+  return MOEGEMM_OK;
+}
+
+int launch(const KernelEntry* e, KParams& p, int grid, void* stream) {
+  hipError_t err = e->launch(p, grid, reinterpret_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(MOEGEMM_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+  return MOEGEMM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int moegemm_abi_version(void) { return MOEGEMM_ABI_VERSION; }
+
+const char* moegemm_last_error(void) { return g_last_error.c_str(); }
+
+int moegemm_kernel_count(int dtype) {
+  int count = 0;
+  table_for(dtype, &count);
+  return count;
+}
+
+int moegemm_kernel_info(int dtype, int index, int32_t* out7) {
+  int count = 0;
+  const KernelEntry* t = table_for(dtype, &count);
+  if (!t || index < 0 || index >= count || !out7)
+    return fail(MOEGEMM_ERR_INVALID, "kernel index %d out of range for dtype %d", index, dtype);
+  const KernelEntry& e = t[index];
+  out7[0] = e.block_m;
+  out7[1] = e.block_n;
+  out7[2] = e.block_k;
+  out7[3] = e.num_warps;
+  out7[4] = e.num_stages;
+  out7[5] = e.lds_bytes;
+  out7[6] = e.waves_m;
+  return MOEGEMM_OK;
+}
+
+int moegemm_grouped_gemm(const int64_t* a_ptrs, const int64_t* b_ptrs, const int64_t* c_ptrs, const int32_t* dims,
+                         const int64_t* strides, int32_t problem_count, int32_t m, int32_t n, int32_t k,
+                         int32_t homogeneous, int32_t total_tiles, int32_t dtype, int32_t input_precision,
+                         int32_t block_m, int32_t block_n, int32_t block_k, int32_t group_size_m, int32_t num_warps,
+                         int32_t num_stages, int32_t grid_size, void* stream) {
+  const KernelEntry* e = nullptr;
+  int rc = check_common(dtype, input_precision, group_size_m, &e, block_m, block_n, block_k, num_warps, num_stages);
+  if (rc != MOEGEMM_OK) return rc;
+  if (problem_count <= 0) return fail(MOEGEMM_ERR_INVALID, "problem_count must be positive (got %d)", problem_count);
+  if (!a_ptrs || !b_ptrs || !c_ptrs) return fail(MOEGEMM_ERR_INVALID, "pointer tables must be non-null");
+  if (total_tiles < 0) return fail(MOEGEMM_ERR_INVALID, "total_tiles must be non-negative");
+  KParams p;
+  std::memset(&p, 0, sizeof(p));
+  p.a_ptrs = a_ptrs;
+  p.b_ptrs = b_ptrs;
+  p.c_ptrs = c_ptrs;
+  p.G = problem_count;
+  p.group_m = group_size_m;
+  p.tf32 = input_precision == MOEGEMM_PRECISION_TF32;
+  if (homogeneous) {
+    if (m <= 0 || n <= 0 || k <= 0)
+      return fail(MOEGEMM_ERR_INVALID, "homogeneous shape must be positive (m=%d n=%d k=%d)", m, n, k);
+    int64_t tiles = (int64_t)problem_count * cdiv(m, block_m) * cdiv(n, block_n);
+    if (tiles > INT32_MAX) return fail(MOEGEMM_ERR_INVALID, "tile count %lld exceeds int32", (long long)tiles);
+    p.mode = MODE_HOMOGENEOUS;
+    p.M = m;
+    p.N = n;
+    p.K = k;
+    p.total_tiles = (int32_t)tiles;
+  } else {
+    if (!dims || !strides) return fail(MOEGEMM_ERR_INVALID, "generic groups need dims and strides tables");
+    p.mode = MODE_GENERIC;
+    p.dims = dims;
+    p.strides = strides;
+    p.total_tiles = total_tiles;
+  }
+  if (p.total_tiles == 0) return MOEGEMM_OK;
+  int grid = grid_size <= 0 ? p.total_tiles : (grid_size < p.total_tiles ? grid_size : p.total_tiles);
+  return launch(e, p, grid, stream);
+}
+
+int moegemm_matmul(const void* a, const void* b, void* c, int32_t m, int32_t n, int32_t k, int64_t stride_am,
+                   int64_t stride_ak, int64_t stride_bk, int64_t stride_bn, int64_t stride_cm, int64_t stride_cn,
+                   int32_t dtype, int32_t input_precision, int32_t block_m, int32_t block_n, int32_t block_k,
+                   int32_t group_size_m, int32_t num_warps, int32_t num_stages, int32_t grid_size, void* stream) {
+  const KernelEntry* e = nullptr;
+  int rc = check_common(dtype, input_precision, group_size_m, &e, block_m, block_n, block_k, num_warps, num_stages);
+  if (rc != MOEGEMM_OK) return rc;
+  if (!a || !b || !c) return fail(MOEGEMM_ERR_INVALID, "matrix pointers must be non-null");
+  if (m <= 0 || n <= 0 || k <= 0) return fail(MOEGEMM_ERR_INVALID, "shape must be positive (m=%d n=%d k=%d)", m, n, k);
+  int64_t tiles = cdiv(m, block_m) * cdiv(n, block_n);
+  if (tiles > INT32_MAX) return fail(MOEGEMM_ERR_INVALID, "tile count %lld exceeds int32", (long long)tiles);
+  KParams p;
+  std::memset(&p, 0, sizeof(p));
+  p.mode = MODE_SINGLE;
+  p.a = a;
+  p.b = b;
+  p.c = c;
+  p.M = m;
+  p.N = n;
+  p.K = k;
+  p.sam = stride_am;
+  p.sak = stride_ak;
+  p.sbk = stride_bk;
+  p.sbn = stride_bn;
+  p.scm = stride_cm;
+  p.scn = stride_cn;
+  p.G = 1;
+  p.group_m = group_size_m;
+  p.tf32 = input_precision == MOEGEMM_PRECISION_TF32;
+  p.total_tiles = (int32_t)tiles;
+  int grid = grid_size <= 0 ? p.total_tiles : (grid_size < p.total_tiles ? grid_size : p.total_tiles);
+  return launch(e, p, grid, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,545 @@
+// Persistent grouped GEMM for gfx950 (CDNA4): C_e = A_e @ B_e over per-problem pointer tables.
+//
+// Semantics follow kernels/grouped_gemm.py:321-482 and kernels/matmul.py:223-273 of the reference:
+// fp32 accumulation of fp16/bf16/fp32 operands, masked M/N/K tails, cast of the accumulator to C's
+// dtype on store, GROUP_M traversal inside each problem, and a persistent grid that walks a flat
+// (problem, m-tile, n-tile) index space.  The implementation is CDNA4-native:
+//
+//  * Work unit: one BM x BN output tile, computed by WM x WN wave64 wavefronts with
+//    v_mfma_f32_32x32x16 / v_mfma_f32_16x16x32 (bf16, f16) or v_mfma_f32_16x16x4_f32 (fp32).
+//  * Operands are swapped (D^T = B^T A^T) so that each lane owns four consecutive N columns of one
+//    output row: the epilogue stores 8-byte (bf16/f16) or 16-byte (fp32) vectors.
+//  * A tiles live in LDS as [BM][BK] (K contiguous) and are read with ds_read_b128; B tiles live
+//    as [BK][BN] (N contiguous, the layout of the caller's B) and are read K-packed with the gfx950
+//    transpose load ds_read_b64_tr_b16, so B never needs a transposed copy in HBM.
+//  * 16-byte chunks are XOR-swizzled inside each LDS row so that fragment reads of 16 consecutive
+//    rows (A) or of 4x2 row/chunk groups (B transpose reads) fall on distinct banks.
+//  * Global -> LDS staging goes through registers with double-buffered LDS stages: the next K
+//    slice is in flight while MFMAs consume the current one; one workgroup barrier per K slice.
+//  * Persistent schedule: workgroup w of a grid of size G processes tiles v, v+G, v+2G, ... where
+//    v renumbers w so that the 8 XCDs (dispatched round-robin by workgroup id) each own a
+//    contiguous run of tiles per round; neighbouring tiles share A/B panels in that XCD's L2.
+//  * Generic groups (heterogeneous shapes/strides) map tile -> problem with an LDS prefix sum of
+//    per-problem tile counts and a binary search, instead of a per-tile scan over all problems.
+//  * Every problem is checked at run time for the vector preconditions (unit inner stride, row
+//    stride and extent multiples of the 16-byte chunk, 16-byte aligned base); a problem that fails
+//    them is staged element by element with arbitrary strides.  Pointer tables are read from
+//    device memory on every tile, so callers may rewrite them between launches.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace moegemm {
+
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef short i16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+enum DType : int { DT_F16 = 0, DT_BF16 = 1, DT_F32 = 2 };
+enum Mode : int { MODE_SINGLE = 0, MODE_HOMOGENEOUS = 1, MODE_GENERIC = 2 };
+
+// Kernel arguments, passed by value.  Strides are in elements.
+struct KParams {
+  const int64_t* a_ptrs;
+  const int64_t* b_ptrs;
+  const int64_t* c_ptrs;
+  const int32_t* dims;     // [G,3] = (m, n, k) per problem (generic mode)
+  const int64_t* strides;  // [G,6] = (am, ak, bk, bn, cm, cn) per problem (generic mode)
+  const void* a;           // single mode operands
+  const void* b;
+  void* c;
+  int64_t sam, sak, sbk, sbn, scm, scn;  // single mode strides
+  int32_t mode;
+  int32_t G;
+  int32_t M, N, K;       // single / homogeneous shape
+  int32_t total_tiles;
+  int32_t group_m;
+  int32_t tf32;          // fp32 only: round operands to TF32 (10-bit mantissa, ties away)
+};
+
+struct ProblemDesc {
+  const char* a;
+  const char* b;
+  char* c;
+  int32_t m, n, k;
+  int64_t sam, sak, sbk, sbn, scm, scn;
+};
+
+// ---------------------------------------------------------------------------------------------
+// Element traits
+struct EBf16 {
+  using raw = uint16_t;
+  static constexpr int dtype = DT_BF16;
+  static constexpr bool is_f32 = false;
+};
+struct EF16 {
+  using raw = uint16_t;
+  static constexpr int dtype = DT_F16;
+  static constexpr bool is_f32 = false;
+};
+struct EF32 {
+  using raw = uint32_t;
+  static constexpr int dtype = DT_F32;
+  static constexpr bool is_f32 = true;
+};
+
+__device__ __forceinline__ uint32_t tf32_round(uint32_t u) {
+  // Round-to-nearest, ties away from zero, to a 10-bit mantissa.  Inf/NaN pass through.
+  if ((u & 0x7f800000u) == 0x7f800000u) return u;
+  return (u + 0x1000u) & 0xffffe000u;
+}
+
+template <class E>
+__device__ __forceinline__ void store4(char* dst, f32x4_t v);
+
+template <>
+__device__ __forceinline__ void store4<EBf16>(char* dst, f32x4_t v) {
+  typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+  bf16x4_t o;
+  o[0] = (__bf16)v[0]; o[1] = (__bf16)v[1]; o[2] = (__bf16)v[2]; o[3] = (__bf16)v[3];
+  *reinterpret_cast<bf16x4_t*>(dst) = o;
+}
+template <>
+__device__ __forceinline__ void store4<EF16>(char* dst, f32x4_t v) {
+  typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+  f16x4_t o;
+  o[0] = (_Float16)v[0]; o[1] = (_Float16)v[1]; o[2] = (_Float16)v[2]; o[3] = (_Float16)v[3];
+  *reinterpret_cast<f16x4_t*>(dst) = o;
+}
+template <>
+__device__ __forceinline__ void store4<EF32>(char* dst, f32x4_t v) {
+  *reinterpret_cast<f32x4_t*>(dst) = v;
+}
+
+template <class E>
+__device__ __forceinline__ void store1(char* dst, float v);
+template <>
+__device__ __forceinline__ void store1<EBf16>(char* dst, float v) { *reinterpret_cast<__bf16*>(dst) = (__bf16)v; }
+template <>
+__device__ __forceinline__ void store1<EF16>(char* dst, float v) { *reinterpret_cast<_Float16*>(dst) = (_Float16)v; }
+template <>
+__device__ __forceinline__ void store1<EF32>(char* dst, float v) { *reinterpret_cast<float*>(dst) = v; }
+
+// ---------------------------------------------------------------------------------------------
+// XOR swizzles on 16-byte chunk indices (see header comment).
+__device__ __forceinline__ int swz_a(int row, int chunks) {
+  int f = (chunks >= 16) ? (row & 15) : (chunks == 8) ? ((row & 7) ^ ((row >> 3) & 1))
+                                     : ((row >> 1) ^ (row >> 3));
+  return f & (chunks - 1);
+}
+__device__ __forceinline__ int swz_b(int row, int chunks) {
+  // h = [0, 3, 6, 5] on row bits 0-1, doubled to chunk pairs, plus row bit 3 moving by 8 chunks.
+  int r = row & 3;
+  int h = (r << 1) ^ r;
+  int f = (h << 1) ^ (((row >> 3) & 1) << 3);
+  return f & (chunks - 1);
+}
+
+// ---------------------------------------------------------------------------------------------
+template <class E, int BM_, int BN_, int BK_, int WM_, int WN_>
+struct GemmTile {
+  using raw_t = typename E::raw;
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
+  static constexpr int ES = sizeof(raw_t);
+  static constexpr int NW = WM * WN;
+  static constexpr int NT = NW * 64;
+  static constexpr int WTM = BM / WM;
+  static constexpr int WTN = BN / WN;
+  static constexpr bool F32 = E::is_f32;
+  static constexpr int MI = F32 ? 16 : ((WTM >= 32 && WTN >= 32) ? 32 : 16);
+  static constexpr int MIK = F32 ? 4 : (MI == 32 ? 16 : 32);
+  static constexpr int FM = WTM / MI;
+  static constexpr int FN = WTN / MI;
+  static constexpr int ACC = MI * MI / 64;
+  static constexpr int EPC = 16 / ES;  // elements per 16-byte chunk
+  static constexpr int CA = BK / EPC;  // chunks per A row
+  static constexpr int CB = BN / EPC;  // chunks per B row
+  static constexpr int A_CHUNKS = BM * CA;
+  static constexpr int B_CHUNKS = BK * CB;
+  static constexpr int A_PT = (A_CHUNKS + NT - 1) / NT;
+  static constexpr int B_PT = (B_CHUNKS + NT - 1) / NT;
+  static constexpr int A_BYTES = BM * BK * ES;
+  static constexpr int B_BYTES = BK * BN * ES;
+  static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+  static constexpr int PREFIX = 1024;  // problems per prefix-sum chunk (generic mode)
+  static constexpr int LDS_BYTES = 2 * STAGE_BYTES + (PREFIX + 1) * 4 + NT * 4;
+
+  static_assert(BM % WM == 0 && BN % WN == 0, "tile must split evenly over waves");
+  static_assert(WTM % MI == 0 && WTN % MI == 0, "wave tile must be a multiple of the MFMA tile");
+  static_assert(BK % MIK == 0 && BK % EPC == 0, "BK must cover whole MFMA K steps and chunks");
+  static_assert(F32 || CB >= 4, "transpose reads need at least 32 columns");
+  static_assert(F32 || MIK % 16 == 0, "B swizzle assumes K steps of 16 rows");
+
+  using acc_t = typename std::conditional<ACC == 16, f32x16_t, f32x4_t>::type;
+
+  // -------------------------------------------------------------------------------------------
+  // Global -> register staging for one K slice.  Each thread owns A_PT + B_PT 16-byte chunks.
+  struct Stage {
+    u32x4_t a[A_PT];
+    u32x4_t b[B_PT];
+  };
+
+  __device__ static __forceinline__ u32x4_t load_chunk_gather(const char* base, int64_t s_outer, int64_t s_inner,
+                                                              int outer, int inner0, int outer_lim, int inner_lim,
+                                                              bool tf32) {
+    // Element-wise masked gather of EPC consecutive inner elements (arbitrary strides).
+    u32x4_t v = {0u, 0u, 0u, 0u};
+    if (outer < outer_lim) {
+      const raw_t* p = reinterpret_cast<const raw_t*>(base) + (int64_t)outer * s_outer;
+      raw_t tmp[EPC];
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) {
+        int in = inner0 + e;
+        tmp[e] = (in < inner_lim) ? p[(int64_t)in * s_inner] : (raw_t)0;
+      }
+      v = *reinterpret_cast<u32x4_t*>(tmp);
+    }
+    if (F32 && tf32) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = tf32_round(v[e]);
+    }
+    return v;
+  }
+
+  __device__ static __forceinline__ void load_stage(Stage& st, const ProblemDesc& pd, bool vec_a, bool vec_b,
+                                                    int m0, int n0, int k0, bool tf32) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < A_PT; ++i) {
+      int cl = tid + i * NT;
+      st.a[i] = u32x4_t{0u, 0u, 0u, 0u};
+      if (A_CHUNKS % NT == 0 || cl < A_CHUNKS) {
+        int r = cl / CA, c = cl % CA;
+        int gm = m0 + r, gk = k0 + c * EPC;
+        if (vec_a) {
+          if (gm < pd.m && gk < pd.k) {
+            const u32x4_t* p = reinterpret_cast<const u32x4_t*>(pd.a + ((int64_t)gm * pd.sam + gk) * ES);
+            st.a[i] = *p;
+            if (F32 && tf32) {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) st.a[i][e] = tf32_round(st.a[i][e]);
+            }
+          }
+        } else {
+          st.a[i] = load_chunk_gather(pd.a, pd.sam, pd.sak, gm, gk, pd.m, pd.k, tf32);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < B_PT; ++i) {
+      int cl = tid + i * NT;
+      st.b[i] = u32x4_t{0u, 0u, 0u, 0u};
+      if (B_CHUNKS % NT == 0 || cl < B_CHUNKS) {
+        int r = cl / CB, c = cl % CB;
+        int gk = k0 + r, gn = n0 + c * EPC;
+        if (vec_b) {
+          if (gk < pd.k && gn < pd.n) {
+            const u32x4_t* p = reinterpret_cast<const u32x4_t*>(pd.b + ((int64_t)gk * pd.sbk + gn) * ES);
+            st.b[i] = *p;
+            if (F32 && tf32) {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) st.b[i][e] = tf32_round(st.b[i][e]);
+            }
+          }
+        } else {
+          st.b[i] = load_chunk_gather(pd.b, pd.sbk, pd.sbn, gk, gn, pd.k, pd.n, tf32);
+        }
+      }
+    }
+  }
+
+  __device__ static __forceinline__ void store_stage(const Stage& st, char* lds_a, char* lds_b) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < A_PT; ++i) {
+      int cl = tid + i * NT;
+      if (A_CHUNKS % NT == 0 || cl < A_CHUNKS) {
+        int r = cl / CA, c = cl % CA;
+        int pc = c ^ swz_a(r, CA);
+        *reinterpret_cast<u32x4_t*>(lds_a + (r * CA + pc) * 16) = st.a[i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < B_PT; ++i) {
+      int cl = tid + i * NT;
+      if (B_CHUNKS % NT == 0 || cl < B_CHUNKS) {
+        int r = cl / CB, c = cl % CB;
+        int pc = c ^ swz_b(r, CB);
+        *reinterpret_cast<u32x4_t*>(lds_b + (r * CB + pc) * 16) = st.b[i];
+      }
+    }
+  }
+
+  // -------------------------------------------------------------------------------------------
+  // MFMA over one K slice held in LDS.
+  __device__ static __forceinline__ void compute_stage(acc_t (&acc)[FM][FN], const char* lds_a, const char* lds_b,
+                                                       int wave_m, int wave_n) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int kk = 0; kk < BK / MIK; ++kk) {
+      if constexpr (F32) {
+        // v_mfma_f32_16x16x4_f32, swapped: first operand B^T (row n = lane%16, k = lane/16),
+        // second operand A^T (col m = lane%16, k = lane/16).
+        float af[FM], bf[FN];
+        const int k = kk * 4 + (lane >> 4);
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm) {
+          int row = wave_m * WTM + fm * 16 + (lane & 15);
+          int c = k >> 2;
+          int pc = c ^ swz_a(row, CA);
+          af[fm] = *reinterpret_cast<const float*>(lds_a + (row * CA + pc) * 16 + (k & 3) * 4);
+        }
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+          int col = wave_n * WTN + fn * 16 + (lane & 15);
+          int c = col >> 2;
+          int pc = c ^ swz_b(k, CB);
+          bf[fn] = *reinterpret_cast<const float*>(lds_b + (k * CB + pc) * 16 + (col & 3) * 4);
+        }
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn)
+            acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x4f32(bf[fn], af[fm], acc[fm][fn], 0, 0, 0);
+      } else {
+        i16x8_t af[FM], bf[FN];
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm) {
+          int row = wave_m * WTM + fm * MI + (lane % MI);
+          int c = (kk * MIK) / 8 + lane / MI;
+          int pc = c ^ swz_a(row, CA);
+          af[fm] = *reinterpret_cast<const i16x8_t*>(lds_a + (row * CA + pc) * 16);
+        }
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+          const int g = lane >> 4, s = lane & 15;
+          int row, col;
+          if constexpr (MI == 32) {
+            row = kk * MIK + 8 * (g >> 1) + (s >> 2);
+            col = wave_n * WTN + fn * 32 + 16 * (g & 1) + 4 * (s & 3);
+          } else {
+            row = kk * MIK + 8 * g + (s >> 2);
+            col = wave_n * WTN + fn * 16 + 4 * (s & 3);
+          }
+          int pc = (col >> 3) ^ swz_b(row, CB);
+          const char* p0 = lds_b + (row * CB + pc) * 16 + (col & 7) * 2;
+          const char* p1 = p0 + 4 * CB * 16;  // rows + 4 (same swizzle: bits 0-1 and 3 unchanged)
+          i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) i16x4_t*)(p0));
+          i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) i16x4_t*)(p1));
+          bf[fn] = i16x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn) {
+            if constexpr (E::dtype == DT_BF16) {
+              if constexpr (MI == 32)
+                acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    __builtin_bit_cast(bf16x8_t, bf[fn]), __builtin_bit_cast(bf16x8_t, af[fm]), acc[fm][fn], 0, 0, 0);
+              else
+                acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    __builtin_bit_cast(bf16x8_t, bf[fn]), __builtin_bit_cast(bf16x8_t, af[fm]), acc[fm][fn], 0, 0, 0);
+            } else {
+              if constexpr (MI == 32)
+                acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                    __builtin_bit_cast(f16x8_t, bf[fn]), __builtin_bit_cast(f16x8_t, af[fm]), acc[fm][fn], 0, 0, 0);
+              else
+                acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    __builtin_bit_cast(f16x8_t, bf[fn]), __builtin_bit_cast(f16x8_t, af[fm]), acc[fm][fn], 0, 0, 0);
+            }
+          }
+      }
+    }
+  }
+
+  // -------------------------------------------------------------------------------------------
+  // Epilogue: lane owns output row m = mbase + lane%MI and, per group of 4 accumulators, four
+  // consecutive columns.
+  __device__ static __forceinline__ void store_tile(const acc_t (&acc)[FM][FN], const ProblemDesc& pd, int m0,
+                                                    int n0, int wave_m, int wave_n) {
+    const int lane = threadIdx.x & 63;
+    const bool vec_c = pd.scn == 1 && (pd.scm % 4) == 0 && (pd.n % 4) == 0 &&
+                       ((reinterpret_cast<uintptr_t>(pd.c) & (4 * ES - 1)) == 0);
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      const int gm = m0 + wave_m * WTM + fm * MI + (lane % MI);
+      if (gm >= pd.m) continue;
+      char* crow = pd.c + (int64_t)gm * pd.scm * ES;
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) {
+#pragma unroll
+        for (int q = 0; q < ACC / 4; ++q) {
+          int nloc = (MI == 32) ? (q * 8 + (lane >> 5) * 4) : ((lane >> 4) * 4);
+          const int gn = n0 + wave_n * WTN + fn * MI + nloc;
+          f32x4_t v = {acc[fm][fn][q * 4 + 0], acc[fm][fn][q * 4 + 1], acc[fm][fn][q * 4 + 2],
+                       acc[fm][fn][q * 4 + 3]};
+          if (vec_c) {
+            if (gn < pd.n) store4<E>(crow + (int64_t)gn * ES, v);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (gn + e < pd.n) store1<E>(crow + (int64_t)(gn + e) * pd.scn * ES, v[e]);
+          }
+        }
+      }
+    }
+  }
+
+  // -------------------------------------------------------------------------------------------
+  __device__ static __forceinline__ void run_tile(const ProblemDesc& pd, int tm, int tn, char* smem, bool tf32) {
+    const int wave = threadIdx.x >> 6;
+    const int wave_m = wave / WN, wave_n = wave % WN;
+    const int m0 = tm * BM, n0 = tn * BN;
+    const bool vec_a = pd.sak == 1 && (pd.k % EPC) == 0 && (pd.sam % EPC) == 0 &&
+                       ((reinterpret_cast<uintptr_t>(pd.a) & 15) == 0);
+    const bool vec_b = pd.sbn == 1 && (pd.n % EPC) == 0 && (pd.sbk % EPC) == 0 &&
+                       ((reinterpret_cast<uintptr_t>(pd.b) & 15) == 0);
+
+    acc_t acc[FM][FN];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int i = 0; i < ACC; ++i) acc[fm][fn][i] = 0.0f;
+
+    char* lds0 = smem;
+    char* lds1 = smem + STAGE_BYTES;
+    const int kt_count = (pd.k + BK - 1) / BK;
+
+    Stage st;
+    load_stage(st, pd, vec_a, vec_b, m0, n0, 0, tf32);
+    store_stage(st, lds0, lds0 + A_BYTES);
+    __syncthreads();
+    for (int kt = 0; kt < kt_count; ++kt) {
+      char* cur = (kt & 1) ? lds1 : lds0;
+      char* nxt = (kt & 1) ? lds0 : lds1;
+      const bool more = kt + 1 < kt_count;
+      if (more) load_stage(st, pd, vec_a, vec_b, m0, n0, (kt + 1) * BK, tf32);
+      compute_stage(acc, cur, cur + A_BYTES, wave_m, wave_n);
+      if (more) store_stage(st, nxt, nxt + A_BYTES);
+      __syncthreads();
+    }
+    store_tile(acc, pd, m0, n0, wave_m, wave_n);
+  }
+};
+
+// ---------------------------------------------------------------------------------------------
+// GROUP_M traversal inside one problem (kernels/grouped_gemm.py:354-360).
+__device__ __forceinline__ void group_m_order(int local, int m_tiles, int n_tiles, int group_m, int& tm, int& tn) {
+  const int width = group_m * n_tiles;
+  const int group_id = local / width;
+  const int first_m = group_id * group_m;
+  const int gsz = min(m_tiles - first_m, group_m);
+  tm = first_m + (local % gsz);
+  tn = (local % width) / gsz;
+}
+
+// Generic mode: s_pref[i] = tile offset of problem first+i, for one chunk of PREFIX problems.
+template <class T>
+__device__ __forceinline__ void load_prefix(const KParams& p, int* s_pref, int* s_tot, int first, int base) {
+  constexpr int PER = (T::PREFIX + T::NT - 1) / T::NT;
+  int vals[PER];
+  int local = 0;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int i = threadIdx.x * PER + j;
+    const int prob = first + i;
+    int cnt = 0;
+    if (i < T::PREFIX && prob < p.G) {
+      const int m = p.dims[prob * 3 + 0], n = p.dims[prob * 3 + 1];
+      cnt = (m > 0 && n > 0) ? ((m + T::BM - 1) / T::BM) * ((n + T::BN - 1) / T::BN) : 0;
+    }
+    local += cnt;
+    vals[j] = local;
+  }
+  s_tot[threadIdx.x] = local;
+  __syncthreads();
+  for (int off = 1; off < T::NT; off <<= 1) {  // Hillis-Steele inclusive scan over NT totals
+    const int v = (threadIdx.x >= (unsigned)off) ? s_tot[threadIdx.x - off] : 0;
+    __syncthreads();
+    s_tot[threadIdx.x] += v;
+    __syncthreads();
+  }
+  const int excl = s_tot[threadIdx.x] - local;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int i = threadIdx.x * PER + j;
+    if (i < T::PREFIX) s_pref[i + 1] = base + excl + vals[j];
+  }
+  if (threadIdx.x == 0) s_pref[0] = base;
+  __syncthreads();
+}
+
+template <class T>
+__global__ void __launch_bounds__(T::NT) grouped_gemm_kernel(KParams p) {
+  __shared__ __attribute__((aligned(16))) char smem[T::LDS_BYTES];
+  int* s_pref = reinterpret_cast<int*>(smem + 2 * T::STAGE_BYTES);
+  int* s_tot = s_pref + T::PREFIX + 1;
+
+  const int grid = gridDim.x;
+  int vid = blockIdx.x;
+  if ((grid & 7) == 0) vid = (blockIdx.x & 7) * (grid >> 3) + (blockIdx.x >> 3);
+
+  int chunk_first = 0;
+  if (p.mode == MODE_GENERIC) load_prefix<T>(p, s_pref, s_tot, 0, 0);
+
+  for (int t = vid; t < p.total_tiles; t += grid) {
+    ProblemDesc pd;
+    int tm, tn;
+    if (p.mode == MODE_SINGLE) {
+      pd.a = static_cast<const char*>(p.a);
+      pd.b = static_cast<const char*>(p.b);
+      pd.c = static_cast<char*>(p.c);
+      pd.m = p.M; pd.n = p.N; pd.k = p.K;
+      pd.sam = p.sam; pd.sak = p.sak; pd.sbk = p.sbk; pd.sbn = p.sbn; pd.scm = p.scm; pd.scn = p.scn;
+      const int mt = (p.M + T::BM - 1) / T::BM, nt = (p.N + T::BN - 1) / T::BN;
+      group_m_order(t, mt, nt, p.group_m, tm, tn);
+    } else if (p.mode == MODE_HOMOGENEOUS) {
+      const int mt = (p.M + T::BM - 1) / T::BM, nt = (p.N + T::BN - 1) / T::BN;
+      const int per = mt * nt;
+      const int e = t / per;
+      group_m_order(t - e * per, mt, nt, p.group_m, tm, tn);
+      pd.a = reinterpret_cast<const char*>(p.a_ptrs[e]);
+      pd.b = reinterpret_cast<const char*>(p.b_ptrs[e]);
+      pd.c = reinterpret_cast<char*>(p.c_ptrs[e]);
+      pd.m = p.M; pd.n = p.N; pd.k = p.K;
+      pd.sam = p.K; pd.sak = 1; pd.sbk = p.N; pd.sbn = 1; pd.scm = p.N; pd.scn = 1;
+    } else {
+      // Advance prefix chunks until this tile falls inside the current one (t is block-uniform).
+      while (t >= s_pref[T::PREFIX] && chunk_first + T::PREFIX < p.G) {
+        const int base = s_pref[T::PREFIX];
+        chunk_first += T::PREFIX;
+        __syncthreads();
+        load_prefix<T>(p, s_pref, s_tot, chunk_first, base);
+      }
+      if (t >= s_pref[T::PREFIX]) break;  // device dims describe fewer tiles than the host count
+      int lo = 0, hi = T::PREFIX;           // largest i with s_pref[i] <= t
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (s_pref[mid] <= t) lo = mid; else hi = mid;
+      }
+      const int e = chunk_first + lo;
+      const int local = t - s_pref[lo];
+      pd.m = p.dims[e * 3 + 0]; pd.n = p.dims[e * 3 + 1]; pd.k = p.dims[e * 3 + 2];
+      const int mt = (pd.m + T::BM - 1) / T::BM, nt = (pd.n + T::BN - 1) / T::BN;
+      group_m_order(local, mt, nt, p.group_m, tm, tn);
+      const int64_t* s = p.strides + (int64_t)e * 6;
+      pd.sam = s[0]; pd.sak = s[1]; pd.sbk = s[2]; pd.sbn = s[3]; pd.scm = s[4]; pd.scn = s[5];
+      pd.a = reinterpret_cast<const char*>(p.a_ptrs[e]);
+      pd.b = reinterpret_cast<const char*>(p.b_ptrs[e]);
+      pd.c = reinterpret_cast<char*>(p.c_ptrs[e]);
+    }
+    T::run_tile(pd, tm, tn, smem, p.tf32 != 0);
+  }
+}
+
+}  // namespace moegemm

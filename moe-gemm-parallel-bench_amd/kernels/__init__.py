@@ -1,0 +1,41 @@
+"""gfx950 HIP grouped/single GEMM kernels and the PyTorch grouped_mm comparison provider."""
+
+from .grouped_gemm import (
+    GroupedWorkspace,
+    build_fused_gate_up_workspace,
+    build_grouped_workspace,
+    grouped_candidate_configs,
+    launch_grouped,
+)
+from .matmul import (
+    KernelConfig,
+    last_matmul_config,
+    launch_matmul,
+    matmul_candidate_configs,
+    select_config,
+)
+from .torch_grouped_gemm import (
+    TorchGroupedMMUnavailable,
+    TorchGroupedWorkspace,
+    build_torch_grouped_workspace,
+    launch_torch_grouped,
+    torch_grouped_mm_unavailable_reason,
+)
+
+__all__ = [
+    "GroupedWorkspace",
+    "KernelConfig",
+    "TorchGroupedMMUnavailable",
+    "TorchGroupedWorkspace",
+    "build_fused_gate_up_workspace",
+    "build_grouped_workspace",
+    "build_torch_grouped_workspace",
+    "grouped_candidate_configs",
+    "last_matmul_config",
+    "launch_grouped",
+    "launch_matmul",
+    "launch_torch_grouped",
+    "matmul_candidate_configs",
+    "select_config",
+    "torch_grouped_mm_unavailable_reason",
+]

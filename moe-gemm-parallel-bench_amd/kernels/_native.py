@@ -1,0 +1,136 @@
+"""ctypes binding of libmoegemm.so (the C ABI declared in include/moegemm.h).
+
+The library is built in-tree next to this file (``csrc/Makefile`` or ``__graft_entry__.build()``).
+Nothing here falls back to another implementation: when the library or a GPU is missing, every
+launch raises ``RuntimeError``, mirroring the reference's "Triton with an active CUDA driver is
+required" error (reference kernels/grouped_gemm.py:626-627, kernels/matmul.py:383-384).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from functools import lru_cache
+from pathlib import Path
+
+LIBRARY_PATH = Path(__file__).resolve().with_name("libmoegemm.so")
+
+ABI_VERSION = 1
+OK = 0
+ERR_INVALID = -1
+ERR_NO_KERNEL = -2
+ERR_LAUNCH = -3
+
+DTYPE_F16 = 0
+DTYPE_BF16 = 1
+DTYPE_F32 = 2
+PRECISION_IEEE = 0
+PRECISION_TF32 = 1
+
+DTYPE_NAMES = {DTYPE_F16: "fp16", DTYPE_BF16: "bf16", DTYPE_F32: "fp32"}
+
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_vp = ctypes.c_void_p
+
+# Exported symbol -> (restype, argtypes).  tests/test_native_abi.py checks this against the header.
+SIGNATURES = {
+    "moegemm_abi_version": (ctypes.c_int, []),
+    "moegemm_last_error": (ctypes.c_char_p, []),
+    "moegemm_kernel_count": (ctypes.c_int, [ctypes.c_int]),
+    "moegemm_kernel_info": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.POINTER(_i32)]),
+    "moegemm_grouped_gemm": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
+    ),
+    "moegemm_matmul": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32,
+         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
+    ),
+}
+
+
+class NativeUnavailable(RuntimeError):
+    """libmoegemm.so is missing or does not match this binding."""
+
+
+@lru_cache(maxsize=1)
+def library() -> ctypes.CDLL:
+    path = Path(os.environ.get("MOEGEMM_LIBRARY", LIBRARY_PATH))
+    if not path.exists():
+        raise NativeUnavailable(
+            f"native library {path} is not built; run `make -C moe-gemm-parallel-bench_amd/csrc` "
+            "or __graft_entry__.build()"
+        )
+    try:
+        lib = ctypes.CDLL(str(path))
+    except OSError as exc:  # missing ROCm runtime, wrong architecture, ...
+        raise NativeUnavailable(f"cannot load {path}: {exc}") from exc
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    version = lib.moegemm_abi_version()
+    if version != ABI_VERSION:
+        raise NativeUnavailable(f"{path} has ABI version {version}, this binding expects {ABI_VERSION}")
+    return lib
+
+
+def available() -> bool:
+    try:
+        library()
+        return True
+    except NativeUnavailable:
+        return False
+
+
+def last_error() -> str:
+    return library().moegemm_last_error().decode("utf-8", "replace")
+
+
+def check(status: int) -> None:
+    """Map a native status to the reference's exception types."""
+    if status == OK:
+        return
+    message = last_error()
+    if status == ERR_INVALID:
+        raise ValueError(message)
+    raise RuntimeError(message)
+
+
+@lru_cache(maxsize=None)
+def compiled_kernels(dtype_code: int) -> tuple[tuple[int, int, int, int, int, int, int], ...]:
+    """(block_m, block_n, block_k, num_warps, num_stages, lds_bytes, waves_m) per compiled kernel."""
+    lib = library()
+    out = (_i32 * 7)()
+    rows = []
+    for index in range(lib.moegemm_kernel_count(dtype_code)):
+        check(lib.moegemm_kernel_info(dtype_code, index, out))
+        rows.append(tuple(int(v) for v in out))
+    return tuple(rows)
+
+
+def dtype_code(dtype) -> int:
+    import torch
+
+    codes = {torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16, torch.float32: DTYPE_F32}
+    if dtype not in codes:
+        raise ValueError(f"unsupported dtype {dtype}; expected float16, bfloat16 or float32")
+    return codes[dtype]
+
+
+def precision_code(input_precision: str, dtype_code_value: int) -> int:
+    if input_precision not in ("ieee", "tf32"):
+        raise ValueError(f"input_precision must be 'ieee' or 'tf32', got {input_precision!r}")
+    # Like tl.dot, TF32 only changes fp32 operands; 16-bit operands are exact in any mode.
+    if input_precision == "tf32" and dtype_code_value == DTYPE_F32:
+        return PRECISION_TF32
+    return PRECISION_IEEE
+
+
+def current_stream_handle(device) -> int:
+    import torch
+
+    return int(torch.cuda.current_stream(device).cuda_stream)

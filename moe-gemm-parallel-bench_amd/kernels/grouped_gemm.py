@@ -1,0 +1,328 @@
+"""Persistent grouped GEMM over distinct expert A/B/C pointers, on gfx950.
+
+Same public surface as the reference's kernels/grouped_gemm.py:
+  * ``GroupedWorkspace`` (reference :67-111): per-problem tensors, int64 pointer tables, int32
+    ``dims`` [G,3] = (m, n, k), int64 ``strides`` [G,6] = (am, ak, bk, bn, cm, cn), provenance.
+  * ``build_grouped_workspace`` / ``build_fused_gate_up_workspace`` (:507-594): seeded device RNG
+    ``normal_() * 0.1`` inputs; W13 packs [gate | up] along N in one B and one C per expert.
+  * ``grouped_candidate_configs`` (:114-224): bounded workload-aware candidates including
+    persistent-grid multipliers.
+  * ``launch_grouped`` (:618-760): G == 1 dispatches to ``launch_matmul`` ("single_problem_matmul");
+    equal contiguous problems use the homogeneous mode ("homogeneous_persistent"); anything else
+    the generic mode with device dims/strides ("generic_persistent").  Exactly one kernel launch
+    per call; ``workspace.config`` / ``workspace.scheduler`` record what ran.
+The device code is one templated HIP kernel (csrc/gemm_kernel.h) behind ``moegemm_grouped_gemm``.
+"""
+
+from __future__ import annotations
+
+import math
+from collections.abc import Sequence
+from dataclasses import dataclass
+
+from . import _native
+from .matmul import (
+    KernelConfig,
+    _is_f32,
+    _require_runtime,
+    _tune,
+    config_pool,
+    diverse_configs,
+    estimate_seconds,
+    last_matmul_config,
+    launch_matmul,
+    matmul_candidate_configs,
+    select_config,
+)
+
+_CTA_MULTIPLIERS = (1, 2, 4)
+
+# Base configs (cta_multiplier == 1) from which grouped candidates are drawn.
+_GROUPED_BASE_CONFIG_POOL: tuple[KernelConfig, ...] = config_pool()
+_GROUPED_BASE_CONFIG_POOL_F32: tuple[KernelConfig, ...] = config_pool("fp32")
+
+
+@dataclass
+class GroupedWorkspace:
+    a: list
+    b: list
+    c: list
+    a_ptrs: object
+    b_ptrs: object
+    c_ptrs: object
+    dims: object
+    strides: object
+    shapes: tuple[tuple[int, int, int], ...]
+    config: KernelConfig
+    shape_signature: int
+    device_signature: int
+    sm_count: int
+    storage_bytes: int
+    homogeneous: bool
+    operation: str = "gemm"
+    scheduler: str = "not_launched"
+
+    @property
+    def problem_count(self) -> int:
+        return len(self.a)
+
+    @property
+    def max_m(self) -> int:
+        return max(m for m, _, _ in self.shapes)
+
+    @property
+    def max_n(self) -> int:
+        return max(n for _, _, n in self.shapes)
+
+    @property
+    def max_k(self) -> int:
+        return max(k for _, k, _ in self.shapes)
+
+    def tile_count_for(self, config: KernelConfig) -> int:
+        return sum(math.ceil(m / config.block_m) * math.ceil(n / config.block_n) for m, _, n in self.shapes)
+
+    @property
+    def tile_count(self) -> int:
+        return self.tile_count_for(self.config)
+
+    def problem_tensors(self):
+        return zip(self.a, self.b, self.c)
+
+
+def grouped_candidate_configs(
+    max_m: int,
+    max_n: int,
+    max_k: int,
+    base_limit: int = 12,
+    *,
+    problem_count: int = 1,
+    sm_count: int = 0,
+    dtype=None,
+) -> tuple[KernelConfig, ...]:
+    """Workload-aware tile and persistent-grid candidates (at most 3 * base_limit).
+
+    Tiles are ranked by ``estimate_seconds`` on the whole group, so a narrow N tile that exposes
+    enough expert tiles to fill the device can outrank a better-padded wide one.  Each kept tile
+    gets cta_multiplier 1 plus 2 (and 4 for skinny tiles) only when the group has more tiles than
+    one grid's worth, so no two candidates launch the same grid.  A single problem dispatches to
+    the single-GEMM path, whose candidates carry cta_multiplier 1 only.
+    """
+    if min(max_m, max_n, max_k, problem_count) <= 0:
+        raise ValueError("grouped candidate dimensions and problem_count must be positive")
+    if sm_count < 0:
+        raise ValueError("sm_count must be non-negative")
+    if problem_count == 1:
+        return tuple(
+            KernelConfig(c.block_m, c.block_n, c.block_k, c.group_size_m, c.num_warps, c.num_stages, 1)
+            for c in matmul_candidate_configs(max_m, max_n, max_k, limit=base_limit, dtype=dtype,
+                                              sm_count=sm_count or 256)
+        )
+    f32 = _is_f32(dtype)
+    element_size = 4 if f32 else 2
+    shapes = [(max_m, max_k, max_n)] * problem_count
+    pool = config_pool(dtype)
+    m_cap = max(16, 2 ** math.ceil(math.log2(max_m)))
+    family = [cfg for cfg in pool if cfg.block_m <= m_cap] or list(pool)
+    fallback = select_config(max_m, max_n, max_k, dtype)
+    if fallback not in family:
+        family.append(fallback)
+    units = sm_count or 256
+    ranked = sorted(
+        family,
+        key=lambda cfg: (estimate_seconds(shapes, cfg, element_size, units, f32),
+                         -cfg.block_m * cfg.block_n, cfg.block_k, cfg.group_size_m),
+    )
+    candidates: list[KernelConfig] = []
+    for cfg in diverse_configs(ranked, base_limit):
+        tiles = problem_count * math.ceil(max_m / cfg.block_m) * math.ceil(max_n / cfg.block_n)
+        multipliers = [1]
+        if not sm_count or tiles > sm_count:
+            multipliers.append(2)
+        if cfg.block_m <= 32 and (not sm_count or tiles > 2 * sm_count):
+            multipliers.append(4)
+        candidates.extend(
+            KernelConfig(cfg.block_m, cfg.block_n, cfg.block_k, cfg.group_size_m, cfg.num_warps,
+                         cfg.num_stages, mult)
+            for mult in multipliers
+        )
+    return tuple(dict.fromkeys(candidates))
+
+
+def _shape_signature(shapes: Sequence[tuple[int, int, int]]) -> int:
+    """31-bit FNV-1a-style fold of every dimension; an autotune-cache discriminator only.
+
+    Same fold as the reference's kernels/grouped_gemm.py:227-233, so cache keys agree.
+    """
+    value = 2166136261
+    for shape in shapes:
+        for dimension in shape:
+            value = ((value ^ int(dimension)) * 16777619) & 0x7FFFFFFF
+    return value
+
+
+def _normalize(shapes) -> tuple[tuple[int, int, int], ...]:
+    if not shapes:
+        raise ValueError("grouped GEMM requires at least one problem")
+    normalized = tuple(tuple(int(v) for v in shape) for shape in shapes)
+    if any(len(s) != 3 or any(v <= 0 for v in s) for s in normalized):
+        raise ValueError("every grouped shape must be a positive (M, K, N) triple")
+    return normalized
+
+
+def workspace_from_tensors(arrays_a, arrays_b, arrays_c, config: KernelConfig | None = None) -> GroupedWorkspace:
+    """Wrap caller-owned per-problem tensors (any strides) in a GroupedWorkspace."""
+    import torch
+
+    if not (len(arrays_a) == len(arrays_b) == len(arrays_c)) or not arrays_a:
+        raise ValueError("A, B and C lists must be non-empty and of equal length")
+    shapes = []
+    for a, b, c in zip(arrays_a, arrays_b, arrays_c):
+        if a.ndim != 2 or b.ndim != 2 or c.ndim != 2 or a.shape[1] != b.shape[0] or tuple(c.shape) != (a.shape[0], b.shape[1]):
+            raise ValueError(f"shape mismatch: A={tuple(a.shape)}, B={tuple(b.shape)}, C={tuple(c.shape)}")
+        shapes.append((int(a.shape[0]), int(a.shape[1]), int(b.shape[1])))
+    normalized = _normalize(shapes)
+    device = arrays_a[0].device
+    dtype = arrays_a[0].dtype
+    for tensor in (*arrays_a, *arrays_b, *arrays_c):
+        if tensor.device != device or tensor.dtype != dtype:
+            raise ValueError("every grouped tensor must share one device and dtype")
+    first_m, first_k, first_n = normalized[0]
+    config = config or select_config(first_m, first_n, first_k, dtype)
+
+    def pointer_table(arrays):
+        return torch.tensor([t.data_ptr() for t in arrays], device=device, dtype=torch.int64)
+
+    a_ptrs, b_ptrs, c_ptrs = pointer_table(arrays_a), pointer_table(arrays_b), pointer_table(arrays_c)
+    dims = torch.tensor([[m, n, k] for m, k, n in normalized], device=device, dtype=torch.int32)
+    strides = torch.tensor(
+        [[a.stride(0), a.stride(1), b.stride(0), b.stride(1), c.stride(0), c.stride(1)]
+         for a, b, c in zip(arrays_a, arrays_b, arrays_c)],
+        device=device, dtype=torch.int64,
+    )
+    tables = [a_ptrs, b_ptrs, c_ptrs, dims, strides]
+    storage_bytes = sum(t.numel() * t.element_size() for t in (*arrays_a, *arrays_b, *arrays_c, *tables))
+    if device.type == "cuda":
+        props = torch.cuda.get_device_properties(device)
+        sm_count = int(props.multi_processor_count)
+        device_signature = (int(props.major) * 10 + int(props.minor)) * 1000 + sm_count
+    else:
+        sm_count, device_signature = 0, 0
+    homogeneous = all(s == normalized[0] for s in normalized) and all(
+        t.is_contiguous() for t in (*arrays_a, *arrays_b, *arrays_c)
+    )
+    return GroupedWorkspace(
+        list(arrays_a), list(arrays_b), list(arrays_c), a_ptrs, b_ptrs, c_ptrs, dims, strides,
+        normalized, config, _shape_signature(normalized), device_signature, sm_count, storage_bytes,
+        homogeneous,
+    )
+
+
+def build_grouped_workspace(
+    shapes: Sequence[tuple[int, int, int]],
+    dtype,
+    seed: int = 0,
+    config: KernelConfig | None = None,
+    *,
+    device: str = "cuda",
+) -> GroupedWorkspace:
+    """Allocate G independent (A, B, C) triples with seeded ``normal_() * 0.1`` inputs.
+
+    ``device="cpu"`` builds the same layout on the host (for the CPU oracle and plumbing checks);
+    launching still requires a GPU.
+    """
+    import torch
+
+    normalized = _normalize(shapes)
+    if device != "cpu" and not torch.cuda.is_available():
+        raise RuntimeError("a ROCm GPU is required to build device workspaces")
+    generator = torch.Generator(device=device).manual_seed(seed)
+    arrays_a, arrays_b, arrays_c = [], [], []
+    for m, k, n in normalized:
+        arrays_a.append(torch.empty((m, k), device=device, dtype=dtype).normal_(generator=generator).mul_(0.1))
+        arrays_b.append(torch.empty((k, n), device=device, dtype=dtype).normal_(generator=generator).mul_(0.1))
+        arrays_c.append(torch.empty((m, n), device=device, dtype=dtype))
+    return workspace_from_tensors(arrays_a, arrays_b, arrays_c, config)
+
+
+def build_fused_gate_up_workspace(
+    shapes: Sequence[tuple[int, int, int]],
+    dtype,
+    seed: int = 0,
+    config: KernelConfig | None = None,
+    *,
+    device: str = "cuda",
+) -> GroupedWorkspace:
+    """Packed W13 problems: each B_e is [H, 2F] = [gate | up], each C_e is [M_e, 2F] = [gate | up]."""
+    normalized = tuple(tuple(int(v) for v in shape) for shape in shapes)
+    if any(len(s) != 3 or s[2] % 2 for s in normalized):
+        raise ValueError("fused Gate+Up shapes require an even packed output dimension")
+    workspace = build_grouped_workspace(normalized, dtype, seed, config, device=device)
+    workspace.operation = "gate_up"
+    return workspace
+
+
+def _grid_size(workspace: GroupedWorkspace, config: KernelConfig) -> int:
+    tiles = workspace.tile_count_for(config)
+    return max(1, min(tiles, workspace.sm_count * config.cta_multiplier))
+
+
+def _check_workspace(workspace: GroupedWorkspace) -> int:
+    a0, b0, c0 = workspace.a[0], workspace.b[0], workspace.c[0]
+    if a0.device.type != "cuda":
+        raise RuntimeError("grouped launches need the workspace on a ROCm GPU")
+    if a0.dtype != b0.dtype or a0.dtype != c0.dtype:
+        raise ValueError("A, B, and C must have the same dtype")
+    return _native.dtype_code(a0.dtype)
+
+
+def _launch_grouped_fixed(workspace: GroupedWorkspace, cfg: KernelConfig, dtype_code: int, precision: int) -> None:
+    lib = _native.library()
+    m, k, n = workspace.shapes[0]
+    status = lib.moegemm_grouped_gemm(
+        workspace.a_ptrs.data_ptr(), workspace.b_ptrs.data_ptr(), workspace.c_ptrs.data_ptr(),
+        workspace.dims.data_ptr(), workspace.strides.data_ptr(),
+        workspace.problem_count, m, n, k, 1 if workspace.homogeneous else 0,
+        workspace.tile_count_for(cfg), dtype_code, precision,
+        cfg.block_m, cfg.block_n, cfg.block_k, cfg.group_size_m, cfg.num_warps, cfg.num_stages,
+        _grid_size(workspace, cfg), _native.current_stream_handle(workspace.a[0].device),
+    )
+    _native.check(status)
+
+
+_GROUPED_AUTOTUNE_CACHE: dict[tuple, KernelConfig] = {}
+
+
+def launch_grouped(
+    workspace: GroupedWorkspace,
+    input_precision: str = "ieee",
+    config: KernelConfig | None = None,
+    *,
+    autotune: bool = True,
+) -> None:
+    """Launch the persistent grouped kernel (autotuned per workload key, or a fixed config)."""
+    _require_runtime()
+    cfg = config or workspace.config
+    if workspace.problem_count == 1:
+        launch_matmul(workspace.a[0], workspace.b[0], workspace.c[0], cfg, input_precision, autotune=autotune)
+        workspace.config = last_matmul_config(cfg) if autotune else cfg
+        workspace.scheduler = "single_problem_matmul"
+        return
+    dtype_code = _check_workspace(workspace)
+    precision = _native.precision_code(input_precision, dtype_code)
+    scheduler = "homogeneous_persistent" if workspace.homogeneous else "generic_persistent"
+    if autotune:
+        key = (
+            scheduler, workspace.problem_count, workspace.max_m, workspace.max_n, workspace.max_k,
+            workspace.shape_signature, workspace.device_signature, workspace.sm_count, dtype_code, precision,
+        )
+        cfg = _GROUPED_AUTOTUNE_CACHE.get(key)
+        if cfg is None:
+            candidates = grouped_candidate_configs(
+                workspace.max_m, workspace.max_n, workspace.max_k,
+                problem_count=workspace.problem_count, sm_count=workspace.sm_count, dtype=workspace.a[0].dtype,
+            )
+            cfg = _tune(candidates, lambda c: _launch_grouped_fixed(workspace, c, dtype_code, precision))
+            _GROUPED_AUTOTUNE_CACHE[key] = cfg
+    _launch_grouped_fixed(workspace, cfg, dtype_code, precision)
+    workspace.config = cfg
+    workspace.scheduler = scheduler

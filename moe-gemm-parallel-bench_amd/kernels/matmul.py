@@ -1,0 +1,313 @@
+"""Masked single GEMM on gfx950: config record, compiled tile menu, candidates and launcher.
+
+Public surface and behaviour follow the reference's kernels/matmul.py:
+  * ``KernelConfig`` (reference :60-73) with the same fields.  On this backend ``num_warps`` is the
+    number of wave64 wavefronts per workgroup and ``num_stages`` the number of LDS stages of the
+    K pipeline; ``group_size_m`` is the GROUP_M traversal width and ``cta_multiplier`` the
+    persistent-grid multiplier of grouped launches.
+  * ``select_config`` (:76-86) is the heuristic fallback; ``matmul_candidate_configs`` (:187-211)
+    returns a bounded shape-family candidate set; ``diverse_configs`` (:142-161) keeps coverage of
+    tile/traversal choices when truncating a ranked list.
+  * ``launch_matmul`` (:373-433) validates like ``_validate_matrices`` (:359-370): ValueError for
+    bad shapes/dtypes/devices, RuntimeError when the native library or a GPU is missing.  With
+    ``autotune=True`` the first call for a shape key measures the candidates (hot graph timing)
+    and later calls are a cache lookup plus exactly one kernel launch (capturable).
+The kernel itself is ``csrc/gemm_kernel.h`` behind ``moegemm_matmul`` (include/moegemm.h).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import asdict, dataclass
+
+from utils.benchmark import hot_autotune_bench
+
+from . import _native
+
+
+@dataclass(frozen=True)
+class KernelConfig:
+    block_m: int
+    block_n: int
+    block_k: int
+    group_size_m: int
+    num_warps: int
+    num_stages: int
+    # Persistent-grid multiplier; only grouped launches use it.
+    cta_multiplier: int = 1
+
+    def as_dict(self) -> dict[str, int]:
+        return asdict(self)
+
+    @property
+    def tile_key(self) -> tuple[int, int, int, int, int]:
+        return (self.block_m, self.block_n, self.block_k, self.num_warps, self.num_stages)
+
+
+# Compiled tile menus: (block_m, block_n, block_k, num_warps, num_stages).  They must equal the
+# X-macro menus of csrc/registry.h; tests/test_native_abi.py compares them with the library.
+_MENU_16BIT: tuple[tuple[int, int, int, int, int], ...] = (
+    (256, 256, 64, 4, 2), (256, 128, 64, 4, 2), (128, 256, 64, 4, 2),
+    (128, 128, 64, 4, 2), (128, 64, 64, 4, 2), (64, 256, 64, 4, 2),
+    (64, 128, 64, 4, 2), (64, 64, 64, 4, 2), (64, 64, 32, 4, 2),
+    (32, 256, 64, 4, 2), (32, 128, 64, 4, 2), (32, 128, 128, 4, 2),
+    (16, 256, 64, 4, 2), (16, 256, 128, 4, 2), (16, 128, 128, 4, 2),
+    (16, 64, 128, 4, 2),
+)
+_MENU_F32: tuple[tuple[int, int, int, int, int], ...] = (
+    (128, 128, 32, 4, 2), (64, 64, 32, 4, 2), (32, 64, 32, 4, 2),
+    (16, 64, 32, 4, 2), (32, 32, 32, 2, 2),
+)
+_GROUP_SIZES = (1, 4, 8)
+
+
+def _menu(dtype=None) -> tuple[tuple[int, int, int, int, int], ...]:
+    return _MENU_F32 if _is_f32(dtype) else _MENU_16BIT
+
+
+def _is_f32(dtype) -> bool:
+    if dtype is None:
+        return False
+    if isinstance(dtype, str):
+        return dtype == "fp32"
+    return str(dtype) == "torch.float32"
+
+
+def config_pool(dtype=None) -> tuple[KernelConfig, ...]:
+    """Every launchable single-GEMM config for a dtype: compiled tiles x GROUP_M widths."""
+    return tuple(
+        KernelConfig(bm, bn, bk, group, warps, stages)
+        for bm, bn, bk, warps, stages in _menu(dtype)
+        for group in _GROUP_SIZES
+    )
+
+
+_MATMUL_CONFIG_POOL: tuple[KernelConfig, ...] = config_pool()
+_MATMUL_CONFIG_POOL_F32: tuple[KernelConfig, ...] = config_pool("fp32")
+
+
+def _snap(block_m: int, block_n: int, block_k: int, dtype=None, group: int = 8) -> KernelConfig:
+    """The compiled tile nearest to a wanted (block_m, block_n, block_k), in log2 distance."""
+    def distance(entry):
+        bm, bn, bk, _, _ = entry
+        return (abs(math.log2(bm / block_m)) + abs(math.log2(bn / block_n)), abs(math.log2(bk / block_k)))
+
+    bm, bn, bk, warps, stages = min(_menu(dtype), key=distance)
+    return KernelConfig(bm, bn, bk, group, warps, stages)
+
+
+def select_config(m: int, n: int, k: int, dtype=None) -> KernelConfig:
+    """Heuristic compiled config used before (or instead of) measurement."""
+    if _is_f32(dtype):
+        if m <= 16:
+            return _snap(16, 64, 32, dtype)
+        if m <= 32:
+            return _snap(32, 64, 32, dtype)
+        if m <= 64 or n <= 64:
+            return _snap(64, 64, 32, dtype)
+        return _snap(128, 128, 32, dtype)
+    wide = 256 if n > 128 else 128 if n > 64 else 64
+    if m <= 16:
+        return _snap(16, wide, 128 if k >= 128 and wide < 256 else 64, dtype)
+    if m <= 32:
+        return _snap(32, 256 if n > 128 else 128, 64, dtype)
+    if m <= 64:
+        return _snap(64, wide, 64, dtype)
+    if m <= 128:
+        return _snap(128, 128 if n > 64 else 64, 64, dtype)
+    if n <= 64:
+        return _snap(128, 64, 64, dtype)
+    return _snap(256, 256 if n > 128 else 128, 64, dtype)
+
+
+def diverse_configs(ordered: list[KernelConfig], limit: int) -> list[KernelConfig]:
+    """Truncate a best-first list to ``limit`` while covering distinct tile/traversal choices.
+
+    Walks the ranking in order and first takes each config that adds a (block_m, block_n),
+    block_k or group_size_m value not yet selected; remaining slots are filled best-first.
+    """
+    limit = max(1, limit)
+    unique = list(dict.fromkeys(ordered))
+    chosen: list[KernelConfig] = []
+    seen: set[tuple[str, object]] = set()
+    for cfg in unique:
+        if len(chosen) >= limit:
+            break
+        keys = {("tile", (cfg.block_m, cfg.block_n)), ("bk", cfg.block_k), ("group", cfg.group_size_m),
+                ("warps", cfg.num_warps), ("stages", cfg.num_stages)}
+        if keys - seen:
+            chosen.append(cfg)
+            seen |= keys
+    for cfg in unique:
+        if len(chosen) >= limit:
+            break
+        if cfg not in chosen:
+            chosen.append(cfg)
+    return chosen
+
+
+# MI355X figures used only to rank candidates before measurement.
+_PEAK_FLOPS_16BIT = 2.5166e15
+_PEAK_FLOPS_F32 = 1.573e14
+_HBM_BYTES_PER_S = 8.0e12
+
+
+def estimate_seconds(
+    shapes, cfg: KernelConfig, element_size: int, sm_count: int, f32: bool = False
+) -> float:
+    """Rough roofline time of a tile config on a group of (M, K, N) problems.
+
+    Compute: padded MFMA work at a tile-size-dependent fraction of peak, inflated by wave
+    quantisation of the output tiles over the compute units.  Memory: A is re-read once per
+    N tile and B once per M tile (L2 reuse ignored), plus one C write.
+    """
+    shapes = list(shapes)
+    tiles = 0
+    padded = 0
+    traffic = 0
+    for m, k, n in shapes:
+        mt, nt, kt = math.ceil(m / cfg.block_m), math.ceil(n / cfg.block_n), math.ceil(k / cfg.block_k)
+        tiles += mt * nt
+        padded += 2 * mt * nt * kt * cfg.block_m * cfg.block_n * cfg.block_k
+        traffic += element_size * (m * k * nt + k * n * mt + m * n)
+    if not tiles:
+        return 0.0
+    units = max(1, sm_count or 256)
+    waves = math.ceil(tiles / units)
+    quantisation = waves * units / tiles
+    wave_tile = (cfg.block_m * cfg.block_n) / max(1, cfg.num_warps)
+    mfma_fraction = min(0.85, 0.25 + wave_tile / 16384.0)
+    peak = _PEAK_FLOPS_F32 if f32 else _PEAK_FLOPS_16BIT
+    compute = padded / (peak * mfma_fraction) * quantisation
+    # A tile's K loop streams at most ~1/units of HBM bandwidth; few tiles cannot use it all.
+    busy = min(1.0, tiles / units)
+    memory = traffic / (_HBM_BYTES_PER_S * max(busy, 1.0 / units))
+    return max(compute, memory)
+
+
+def matmul_candidate_configs(m: int, n: int, k: int, limit: int = 10, *, dtype=None,
+                             sm_count: int = 256) -> tuple[KernelConfig, ...]:
+    """Bounded candidate set for one [m, k] @ [k, n] shape, best predicted first."""
+    f32 = _is_f32(dtype)
+    element_size = 4 if f32 else 2
+    pool = config_pool(dtype)
+    # Shape family: drop tiles whose M or N edge is more than twice the (rounded-up) extent.
+    family = [
+        cfg for cfg in pool
+        if cfg.block_m <= max(16, 2 ** math.ceil(math.log2(max(m, 1))))
+        and cfg.block_n <= max(64, 2 ** math.ceil(math.log2(max(n, 1))))
+    ] or list(pool)
+    fallback = select_config(m, n, k, dtype)
+    if fallback not in family:
+        family.append(fallback)
+    ranked = sorted(
+        family,
+        key=lambda cfg: (estimate_seconds([(m, k, n)], cfg, element_size, sm_count, f32),
+                         -cfg.block_m * cfg.block_n, cfg.block_k, cfg.group_size_m),
+    )
+    return tuple(diverse_configs(ranked, limit))
+
+
+# -------------------------------------------------------------------------------------------------
+# Launch
+
+_AUTOTUNE_CACHE: dict[tuple, KernelConfig] = {}
+_LAST_AUTOTUNED: list[KernelConfig | None] = [None]
+
+
+def _device_signature(device) -> int:
+    import torch
+
+    props = torch.cuda.get_device_properties(device)
+    return (int(props.major) * 10 + int(props.minor)) * 1000 + int(props.multi_processor_count)
+
+
+def last_matmul_config(fallback: KernelConfig) -> KernelConfig:
+    """Config selected by the most recent autotuned ``launch_matmul`` (else ``fallback``)."""
+    return _LAST_AUTOTUNED[0] or fallback
+
+
+def _validate_matrices(a, b, c) -> tuple[int, int, int]:
+    if a.ndim != 2 or b.ndim != 2 or c.ndim != 2:
+        raise ValueError("A, B, and C must be matrices")
+    m, k = a.shape
+    kb, n = b.shape
+    if k != kb or tuple(c.shape) != (m, n):
+        raise ValueError(f"shape mismatch: A={tuple(a.shape)}, B={tuple(b.shape)}, C={tuple(c.shape)}")
+    if a.device != b.device or a.device != c.device or a.device.type != "cuda":
+        raise ValueError("A, B, and C must be on the same GPU device")
+    if a.dtype != b.dtype or a.dtype != c.dtype:
+        raise ValueError("A, B, and C must have the same dtype")
+    return int(m), int(n), int(k)
+
+
+def _require_runtime() -> None:
+    import torch
+
+    if not torch.cuda.is_available():
+        raise RuntimeError("a ROCm GPU is required to launch the native GEMM kernels")
+    try:
+        _native.library()
+    except _native.NativeUnavailable as exc:
+        raise RuntimeError(str(exc)) from exc
+
+
+def _launch_fixed(a, b, c, m, n, k, cfg: KernelConfig, dtype_code: int, precision: int) -> None:
+    lib = _native.library()
+    status = lib.moegemm_matmul(
+        a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k,
+        a.stride(0), a.stride(1), b.stride(0), b.stride(1), c.stride(0), c.stride(1),
+        dtype_code, precision,
+        cfg.block_m, cfg.block_n, cfg.block_k, cfg.group_size_m, cfg.num_warps, cfg.num_stages,
+        0, _native.current_stream_handle(a.device),
+    )
+    _native.check(status)
+
+
+def launch_matmul(
+    a,
+    b,
+    c,
+    config: KernelConfig | None = None,
+    input_precision: str = "ieee",
+    *,
+    autotune: bool = True,
+) -> None:
+    """Launch C = A @ B: autotuned per shape key, or with an explicit config when autotune is false."""
+    m, n, k = _validate_matrices(a, b, c)
+    _require_runtime()
+    dtype_code = _native.dtype_code(a.dtype)
+    precision = _native.precision_code(input_precision, dtype_code)
+    if not autotune:
+        cfg = config or select_config(m, n, k, a.dtype)
+        _launch_fixed(a, b, c, m, n, k, cfg, dtype_code, precision)
+        return
+    key = (
+        m, n, k, tuple(a.stride()), tuple(b.stride()), tuple(c.stride()), dtype_code, precision,
+        _device_signature(a.device),
+    )
+    best = _AUTOTUNE_CACHE.get(key)
+    if best is None:
+        best = _tune(
+            matmul_candidate_configs(m, n, k, dtype=a.dtype,
+                                     sm_count=_device_signature(a.device) % 1000),
+            lambda cfg: _launch_fixed(a, b, c, m, n, k, cfg, dtype_code, precision),
+        )
+        _AUTOTUNE_CACHE[key] = best
+    _LAST_AUTOTUNED[0] = best
+    _launch_fixed(a, b, c, m, n, k, best, dtype_code, precision)
+
+
+def _tune(candidates, launch) -> KernelConfig:
+    """Hot-time every candidate (graph-captured, bounded) and return the fastest."""
+    best, best_ms = None, math.inf
+    for cfg in candidates:
+        try:
+            median_ms = hot_autotune_bench(lambda cfg=cfg: launch(cfg), (0.5,))[0]
+        except (RuntimeError, ValueError):
+            continue
+        if median_ms < best_ms:
+            best, best_ms = cfg, median_ms
+    if best is None:
+        raise RuntimeError("every autotune candidate failed to launch")
+    return best

@@ -1,0 +1,224 @@
+"""CPU ORACLE - TEST INFRASTRUCTURE ONLY.
+
+Python side of the oracle: a ctypes binding of ``grouped_gemm_oracle.c`` (built by ``make`` in
+this directory into ``liboracle.so``) plus numpy restatements of the reference's table layout and
+launch rules.  Only tests/, ``__graft_entry__.smoke()`` and bench.py's ``cpu_baseline`` leg may
+import this module, and only as the checker; the product path never does.
+
+Functions and the reference code they restate:
+  * ``gemm`` / ``grouped_gemm``     kernels/grouped_gemm.py:399-482 and kernels/matmul.py:264-314
+                                    (fp32-exact products, fp32/fp64 accumulation, cast on store);
+                                    pinned by tests/test_oracle.py against the golden fixtures
+                                    (torch CPU float64), closed forms, brute force and numpy.
+  * ``tables``                      kernels/grouped_gemm.py:530-544 (pointer order, dims (m, n, k),
+                                    strides (am, ak, bk, bn, cm, cn)); pinned by brute force.
+  * ``is_homogeneous``              kernels/grouped_gemm.py:550-552; pinned by reference tests'
+                                    expectations (tests/test_gpu.py:99-125 of the reference).
+  * ``dispatch``                    kernels/grouped_gemm.py:629-640, 652, 712 (scheduler names).
+  * ``grid_size``                   kernels/grouped_gemm.py:597-599.
+  * ``tile_order``                  kernels/grouped_gemm.py:353-360 (GROUP_M traversal + persistent
+                                    stride); pinned by a coverage/bijection check.
+  * ``w13_reference``               benchmark_moe.py:258-266 (cat of gate and up products).
+  * ``to_bf16_bits`` / ``to_f16_bits``  round-to-nearest-even casts; pinned against torch/numpy.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import subprocess
+from functools import lru_cache
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIBRARY = HERE / "liboracle.so"
+
+F16, BF16, F32 = 0, 1, 2
+ACCUM_F64, ACCUM_F32 = 0, 1
+_DTYPES = {"fp16": F16, "bf16": BF16, "fp32": F32}
+
+
+@lru_cache(maxsize=1)
+def lib() -> ctypes.CDLL:
+    if not LIBRARY.exists():
+        subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    handle = ctypes.CDLL(str(LIBRARY))
+    vp, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+    handle.oracle_gemm.argtypes = [vp, vp, vp, i32, i32, i32, i64, i64, i64, i64, i64, i64, i32, i32, i32, vp]
+    handle.oracle_gemm.restype = ctypes.c_int
+    handle.oracle_grouped_gemm.argtypes = [i32, vp, vp, vp, vp, vp, i32, i32, i32]
+    handle.oracle_grouped_gemm.restype = ctypes.c_int
+    handle.oracle_gemm_rowmajor_fast.argtypes = [vp, vp, vp, i32, i32, i32, i32, vp, i32]
+    handle.oracle_gemm_rowmajor_fast.restype = ctypes.c_int
+    handle.oracle_float_to_bf16.argtypes = [ctypes.c_float]
+    handle.oracle_float_to_bf16.restype = ctypes.c_uint16
+    handle.oracle_float_to_f16.argtypes = [ctypes.c_float]
+    handle.oracle_float_to_f16.restype = ctypes.c_uint16
+    handle.oracle_tf32_round.argtypes = [ctypes.c_float]
+    handle.oracle_tf32_round.restype = ctypes.c_float
+    return handle
+
+
+# --------------------------------------------------------------------------------------------
+# Element encodings.  16-bit matrices are carried as numpy uint16 bit patterns.
+
+def bf16_bits_to_float(bits: np.ndarray) -> np.ndarray:
+    return (bits.astype(np.uint32) << 16).view(np.float32)
+
+
+def f16_bits_to_float(bits: np.ndarray) -> np.ndarray:
+    return bits.view(np.float16).astype(np.float32)
+
+
+def to_float(bits: np.ndarray, dtype: str) -> np.ndarray:
+    if dtype == "bf16":
+        return bf16_bits_to_float(bits)
+    if dtype == "fp16":
+        return f16_bits_to_float(bits)
+    return bits.astype(np.float32)
+
+
+def to_bf16_bits(values: np.ndarray) -> np.ndarray:
+    handle = lib()
+    flat = np.ascontiguousarray(values, dtype=np.float32).ravel()
+    return np.array([handle.oracle_float_to_bf16(float(v)) for v in flat], dtype=np.uint16).reshape(np.shape(values))
+
+
+def to_f16_bits(values: np.ndarray) -> np.ndarray:
+    handle = lib()
+    flat = np.ascontiguousarray(values, dtype=np.float32).ravel()
+    return np.array([handle.oracle_float_to_f16(float(v)) for v in flat], dtype=np.uint16).reshape(np.shape(values))
+
+
+def tf32_round(values: np.ndarray) -> np.ndarray:
+    handle = lib()
+    flat = np.ascontiguousarray(values, dtype=np.float32).ravel()
+    return np.array([handle.oracle_tf32_round(float(v)) for v in flat], dtype=np.float32).reshape(np.shape(values))
+
+
+# --------------------------------------------------------------------------------------------
+# GEMM
+
+def _element_size(dtype: str) -> int:
+    return 4 if dtype == "fp32" else 2
+
+
+def gemm(a: np.ndarray, b: np.ndarray, dtype: str, *, tf32: bool = False, accum: str = "f64",
+         out_strides: tuple[int, int] | None = None, return_sums: bool = False):
+    """C = A @ B for one problem.  ``a``/``b`` are uint16 bit patterns (fp16/bf16) or float32,
+    with any (element) strides numpy allows; returns C in the operand encoding (and optionally
+    the unrounded sums as float64)."""
+    code = _DTYPES[dtype]
+    store = np.float32 if dtype == "fp32" else np.uint16
+    a = np.asarray(a)
+    b = np.asarray(b)
+    if a.dtype != store or b.dtype != store:
+        raise TypeError(f"{dtype} operands must be numpy {np.dtype(store).name} arrays")
+    m, k = a.shape
+    kb, n = b.shape
+    if k != kb:
+        raise ValueError("inner dimensions differ")
+    es = _element_size(dtype)
+    c = np.zeros((m, n), dtype=store)
+    sums = np.zeros((m, n), dtype=np.float64) if return_sums else None
+    rc = lib().oracle_gemm(
+        a.ctypes.data, b.ctypes.data, c.ctypes.data, m, n, k,
+        a.strides[0] // es, a.strides[1] // es, b.strides[0] // es, b.strides[1] // es, n, 1,
+        code, int(tf32), ACCUM_F32 if accum == "f32" else ACCUM_F64,
+        sums.ctypes.data if sums is not None else None,
+    )
+    if rc:
+        raise ValueError("oracle_gemm rejected its arguments")
+    return (c, sums) if return_sums else c
+
+
+def grouped_gemm(a_list, b_list, dtype: str, **kwargs):
+    """Per-problem ``gemm`` over a group (the reference's grouped kernel semantics)."""
+    if not a_list or len(a_list) != len(b_list):
+        raise ValueError("grouped GEMM requires matching, non-empty operand lists")
+    return [gemm(a, b, dtype, **kwargs) for a, b in zip(a_list, b_list)]
+
+
+def w13_reference(a: np.ndarray, b: np.ndarray, dtype: str, **kwargs) -> np.ndarray:
+    """Packed Gate+Up reference: [A @ B[:, :F] | A @ B[:, F:]] (benchmark_moe.py:258-266)."""
+    n = b.shape[1]
+    if n % 2:
+        raise ValueError("packed W13 needs an even output width")
+    half = n // 2
+    gate = gemm(a, np.ascontiguousarray(b[:, :half]), dtype, **kwargs)
+    up = gemm(a, np.ascontiguousarray(b[:, half:]), dtype, **kwargs)
+    return np.concatenate([gate, up], axis=1)
+
+
+def gemm_fast_bf16(a_bits: np.ndarray, b_bits: np.ndarray, threads: int, dtype: str = "bf16") -> np.ndarray:
+    """OpenMP fp32-accumulating contiguous GEMM (CPU baseline timing only)."""
+    m, k = a_bits.shape
+    _, n = b_bits.shape
+    a_bits = np.ascontiguousarray(a_bits, dtype=np.uint16)
+    b_bits = np.ascontiguousarray(b_bits, dtype=np.uint16)
+    c = np.empty((m, n), dtype=np.uint16)
+    scratch = np.empty((m, n), dtype=np.float32)
+    rc = lib().oracle_gemm_rowmajor_fast(a_bits.ctypes.data, b_bits.ctypes.data, c.ctypes.data, m, n, k,
+                                         _DTYPES[dtype], scratch.ctypes.data, threads)
+    if rc:
+        raise ValueError("oracle_gemm_rowmajor_fast rejected its arguments")
+    return c
+
+
+# --------------------------------------------------------------------------------------------
+# Tables and launch rules
+
+def tables(shapes, strides_list=None):
+    """dims [G,3] = (m, n, k) and strides [G,6] = (am, ak, bk, bn, cm, cn) as the reference builds them."""
+    dims = np.array([[m, n, k] for m, k, n in shapes], dtype=np.int32)
+    if strides_list is None:
+        strides_list = [(k, 1, n, 1, n, 1) for m, k, n in shapes]
+    strides = np.array(strides_list, dtype=np.int64)
+    return dims, strides
+
+
+def is_homogeneous(shapes, contiguous_flags) -> bool:
+    return all(s == shapes[0] for s in shapes) and all(contiguous_flags)
+
+
+def dispatch(problem_count: int, homogeneous: bool) -> str:
+    if problem_count == 1:
+        return "single_problem_matmul"
+    return "homogeneous_persistent" if homogeneous else "generic_persistent"
+
+
+def tile_count(shapes, block_m: int, block_n: int) -> int:
+    return sum(math.ceil(m / block_m) * math.ceil(n / block_n) for m, _, n in shapes)
+
+
+def grid_size(shapes, block_m: int, block_n: int, sm_count: int, cta_multiplier: int) -> int:
+    return max(1, min(tile_count(shapes, block_m, block_n), sm_count * cta_multiplier))
+
+
+def group_m_tile(local: int, m_tiles: int, n_tiles: int, group_m: int) -> tuple[int, int]:
+    width = group_m * n_tiles
+    first_m = (local // width) * group_m
+    size = min(m_tiles - first_m, group_m)
+    return first_m + local % size, (local % width) // size
+
+
+def tile_order(shapes, block_m: int, block_n: int, group_m: int, grid: int):
+    """For each program id, the (problem, m-tile, n-tile) list it visits in order."""
+    offsets = [0]
+    per_problem = []
+    for m, _, n in shapes:
+        mt, nt = math.ceil(m / block_m), math.ceil(n / block_n)
+        per_problem.append((mt, nt))
+        offsets.append(offsets[-1] + mt * nt)
+    total = offsets[-1]
+    visits = []
+    for pid in range(grid):
+        mine = []
+        for t in range(pid, total, grid):
+            e = int(np.searchsorted(offsets, t, side="right") - 1)
+            mt, nt = per_problem[e]
+            mine.append((e, *group_m_tile(t - offsets[e], mt, nt, group_m)))
+        visits.append(mine)
+    return visits
