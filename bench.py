@@ -1,0 +1,229 @@
+"""Headline benchmark: one MI355X, DeepSeek-V3 EP W13 (packed Gate+Up) grouped GEMM, M_e = 512, bf16.
+
+``python bench.py [--gpus 1] [--steps K] [--warmup W]`` prints ONE JSON line.
+
+* Workload (one EP rank of BASELINE configs[2], the north-star target case): 32 experts of
+  [512, 7168] @ [7168, 4096] in bf16 with fp32 accumulation, synthetic ``normal_() * 0.1`` inputs
+  resident in HBM.  A step is one ``launch_grouped`` call over the whole group (one kernel launch).
+* ``value`` is whole-job TFLOP/s = 2 * sum_e M_e*K*N / (time per step), from HIP events recorded on
+  the launch stream around exactly K back-to-back steps (synchronised before and after).
+* ``roofline`` prices that kernel against the dense bf16 MFMA peak (2.5 PFLOP/s); ``traffic`` is
+  the measured HBM bytes per launch from profiles/ (rocprofv3 FETCH_SIZE + WRITE_SIZE, scaled by a
+  copy-kernel calibration) or null when no such profile is committed.
+* ``cases`` adds the HBM-bound M_e = 8 EP case, the TP counterparts (EP/TP ratio) and the DSV3 W2
+  cases, each timed the same way and checked against a float32 torch reference on a sample of
+  experts.
+* ``cpu_baseline`` times the CPU oracle's blocked fp32-accumulating GEMM on the host cores on a
+  bounded sample of the same workload (rank 0, N = 1 only).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path[:0] = [str(REPO / "moe-gemm-parallel-bench_amd"), str(REPO)]
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+METRIC = "grouped-GEMM TFLOP/s + % MFMA/HBM roofline, EP vs TP per-rank, 1 MI355X"
+
+# DeepSeek-V3: H=7168, F=2048, E=256, topk=8, P=8.
+DSV3 = dict(hidden=7168, ffn=2048, experts=256, parallel=8)
+
+
+def _shapes(projection: str, parallel_type: str, m: int):
+    from utils.metrics import moe_shapes
+
+    return moe_shapes(projection, parallel_type, m, DSV3["hidden"], DSV3["ffn"], DSV3["experts"], DSV3["parallel"])
+
+
+def _workspace(projection: str, parallel_type: str, m: int, seed: int):
+    import torch
+
+    from kernels.grouped_gemm import build_fused_gate_up_workspace, build_grouped_workspace
+
+    builder = build_fused_gate_up_workspace if projection == "W1" else build_grouped_workspace
+    return builder(_shapes(projection, parallel_type, m), torch.bfloat16, seed)
+
+
+def _check_sample(workspace, experts=(0, -1)) -> float:
+    """Normwise error of sampled experts against a float32 torch product (GPU)."""
+    worst = 0.0
+    for index in experts:
+        a, b, c = workspace.a[index], workspace.b[index], workspace.c[index]
+        ref = a.float() @ b.float()
+        err = float((c.float() - ref).abs().max()) / float(ref.abs().max())
+        worst = max(worst, err)
+    return worst
+
+
+def _time_steps(workspace, steps: int, warmup: int) -> tuple[float, float]:
+    """(ms per step from HIP events on the launch stream, wall ms per step)."""
+    import torch
+
+    from kernels.grouped_gemm import launch_grouped
+
+    for _ in range(warmup):
+        launch_grouped(workspace, autotune=True)
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall = time.perf_counter()
+    start.record(stream)
+    for _ in range(steps):
+        launch_grouped(workspace, autotune=True)
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - wall) * 1e3
+    return start.elapsed_time(end) / steps, wall / steps
+
+
+def _case(projection: str, parallel_type: str, m: int, steps: int, warmup: int, seed: int = 1234) -> dict:
+    import torch
+
+    from kernels.grouped_gemm import launch_grouped
+    from utils.metrics import gemm_bytes, gemm_flops
+
+    workspace = _workspace(projection, parallel_type, m, seed)
+    launch_grouped(workspace, autotune=True)  # autotune (untimed) on a cache miss
+    for c in workspace.c:
+        c.fill_(float("nan"))
+    launch_grouped(workspace, autotune=True)
+    torch.cuda.synchronize()
+    error = _check_sample(workspace)
+    ms, wall_ms = _time_steps(workspace, steps, warmup)
+    flops = sum(gemm_flops(*s) for s in workspace.shapes)
+    nbytes = sum(gemm_bytes(*s, 2) for s in workspace.shapes)
+    tflops = flops / (ms * 1e9)
+    gbs = nbytes / (ms * 1e6)
+    bound = "mfma" if flops / (PEAK_BF16_TFLOPS * 1e12) >= nbytes / (PEAK_HBM_GBS * 1e9) else "hbm"
+    row = {
+        "case": f"dsv3_{projection.lower()}_{parallel_type.lower()}_me{m}",
+        "experts": workspace.problem_count, "shape_mkn": list(workspace.shapes[0]),
+        "ms": ms, "wall_ms": wall_ms, "tflops": tflops, "gbs": gbs, "bound": bound,
+        "frac": tflops / PEAK_BF16_TFLOPS if bound == "mfma" else gbs / PEAK_HBM_GBS,
+        "config": workspace.config.as_dict(), "scheduler": workspace.scheduler,
+        "normwise_error_sampled": error, "correct": bool(error <= 1e-2),
+        "flops": flops, "ideal_bytes": nbytes,
+    }
+    del workspace
+    torch.cuda.empty_cache()
+    return row
+
+
+def _traffic_from_profiles(case: str):
+    """HBM bytes per launch recorded by a committed rocprofv3 counter summary, if any."""
+    path = REPO / "profiles" / f"{case}_hbm_traffic.md"
+    if not path.exists():
+        return None
+    match = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", path.read_text())
+    return float(match.group(1)) if match else None
+
+
+def _cpu_baseline(seconds_target: float = 12.0) -> dict:
+    """Oracle blocked GEMM on the host cores over a bounded sample of the workload."""
+    import numpy as np
+
+    from oracle import oracle
+
+    threads = len(os.sched_getaffinity(0))
+    m, k, n = 512, DSV3["hidden"], 2 * DSV3["ffn"]
+    rng = np.random.default_rng(1234)
+
+    def bf16(shape):
+        return (rng.standard_normal(shape, dtype=np.float32) * 0.1).view(np.uint32).__rshift__(16).astype(np.uint16)
+
+    a = bf16((m, k))
+    b = bf16((k, n))
+    # Sample: whole [512, 7168] @ [7168, cols] expert slices, growing until ~seconds_target.
+    cols = 256
+    oracle.gemm_fast_bf16(a[:16], b[:, :cols], threads)  # warm (thread pool, pages)
+    done_flops, elapsed, slices = 0, 0.0, 0
+    while elapsed < seconds_target and slices < 64:
+        t0 = time.perf_counter()
+        oracle.gemm_fast_bf16(a, np.ascontiguousarray(b[:, (slices * cols) % n:(slices * cols) % n + cols]), threads)
+        elapsed += time.perf_counter() - t0
+        done_flops += 2 * m * k * cols
+        slices += 1
+    return {
+        "value": done_flops / elapsed / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{slices} slices of one expert's [512,7168]@[7168,{cols}] bf16 GEMM "
+                  f"({done_flops / 1e9:.1f} GFLOP, {elapsed:.1f} s), oracle blocked fp32-accumulating C GEMM",
+    }
+
+
+def main(argv=None) -> int:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--no-cases", action="store_true", help="only the headline case")
+    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = parser.parse_args(argv)
+    if args.gpus != 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path (every GPU box here has "
+              "one GPU); run with --gpus 1.", file=sys.stderr)
+        return 2
+    if args.steps < 1 or args.warmup < 0:
+        raise SystemExit("--steps must be >= 1 and --warmup >= 0")
+    import torch
+
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a ROCm GPU")
+    torch.cuda.set_device(0)
+    headline = _case("W1", "EP", 512, args.steps, args.warmup)
+    cases = []
+    if not args.no_cases:
+        for projection, parallel_type, m in (("W1", "EP", 8), ("W1", "TP", 512), ("W1", "TP", 8),
+                                            ("W2", "EP", 512), ("W2", "TP", 512), ("W2", "EP", 8)):
+            cases.append(_case(projection, parallel_type, m, max(5, args.steps // 2), 2))
+    traffic = _traffic_from_profiles(headline["case"])
+    tp = next((c for c in cases if c["case"] == "dsv3_w1_tp_me512"), None)
+    line = {
+        "metric": METRIC,
+        "value": headline["tflops"],
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": headline["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic normal*0.1 inputs and weights (no checkpoints), resident in HBM",
+        "config": {
+            "workload": "DeepSeek-V3 EP rank, W13 packed Gate+Up, 32 experts x [512,7168]@[7168,4096], bf16, fp32 acc",
+            "model": "deepseek-v3 expert shapes (H=7168, F=2048, E=256, topk=8, P=8)",
+            "tokens_per_expert": 512, "global_batch": 32 * 512, "seq_len": None, "parallelism": "ep8 (one rank)",
+            "kernel_config": headline["config"], "scheduler": headline["scheduler"],
+        },
+        "roofline": {
+            "bound": "mfma", "achieved": headline["tflops"], "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+            "frac": headline["tflops"] / PEAK_BF16_TFLOPS, "traffic": traffic,
+        },
+        "correct": headline["correct"],
+        "normwise_error_sampled": headline["normwise_error_sampled"],
+        "ep_tp_ratio_w13_me512": (tp["tflops"] / headline["tflops"]) if tp else None,
+        "cases": cases,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = _cpu_baseline()
+    print(json.dumps(line))
+    return 0 if headline["correct"] and all(c["correct"] for c in cases) else 1
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

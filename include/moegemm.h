@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define MOEGEMM_ABI_VERSION 1
+#define MOEGEMM_ABI_VERSION 2
 
 #define MOEGEMM_OK 0
 #define MOEGEMM_ERR_INVALID (-1)   /* bad shape, pointer, dtype or parameter (Python: ValueError) */
@@ -64,19 +64,24 @@ int moegemm_kernel_info(int dtype, int index, int32_t* out7);
  *       ceil(m/block_m) * ceil(n/block_n); m, n, k are ignored.
  * group_size_m is the GROUP_M traversal width inside each problem; grid_size is the persistent
  * grid (reference _grid_size, kernels/grouped_gemm.py:597-599); <= 0 means one workgroup per tile.
+ * vector_layout != 0 promises that every problem is fp16/bf16 with unit inner strides, row
+ * pitches and K, N multiples of 8 elements, C row pitch a multiple of 4, 16-byte aligned A/B and
+ * 8-byte aligned C bases, and matrices under 2 GiB: the launch then uses the LDS-DMA kernel.
+ * Otherwise (or for fp32) the general kernel runs, which accepts any strides and alignment.
  */
 int moegemm_grouped_gemm(const int64_t* a_ptrs, const int64_t* b_ptrs, const int64_t* c_ptrs,
                          const int32_t* dims, const int64_t* strides, int32_t problem_count,
                          int32_t m, int32_t n, int32_t k, int32_t homogeneous, int32_t total_tiles,
                          int32_t dtype, int32_t input_precision, int32_t block_m, int32_t block_n,
                          int32_t block_k, int32_t group_size_m, int32_t num_warps,
-                         int32_t num_stages, int32_t grid_size, void* stream);
+                         int32_t num_stages, int32_t grid_size, int32_t vector_layout, void* stream);
 
 /*
  * Masked single GEMM with arbitrary strides, C = A @ B.  Replaces the Triton launch of
  * reference kernels/matmul.py:373-433 (launch_matmul -> _matmul_kernel_impl, :264-314); shape
  * and dtype validation (kernels/matmul.py:359-370) stays in Python.  grid_size <= 0 launches one
  * workgroup per output tile like the reference's 1-D grid; a positive value makes it persistent.
+ * The LDS-DMA kernel is chosen automatically when the operands meet its layout preconditions.
  */
 int moegemm_matmul(const void* a, const void* b, void* c, int32_t m, int32_t n, int32_t k,
                    int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,

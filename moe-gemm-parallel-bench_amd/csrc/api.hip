@@ -69,10 +69,24 @@ int check_common(int dtype, int input_precision, int group_size_m, const KernelE
   return MOEGEMM_OK;
 }
 
-int launch(const KernelEntry* e, KParams& p, int grid, void* stream) {
-  hipError_t err = e->launch(p, grid, reinterpret_cast<hipStream_t>(stream));
+int launch(const KernelEntry* e, KParams& p, int grid, bool vector_layout, void* stream) {
+  LaunchFn fn = (vector_layout && e->launch_fast) ? e->launch_fast : e->launch_general;
+  hipError_t err = fn(p, grid, reinterpret_cast<hipStream_t>(stream));
   if (err != hipSuccess) return fail(MOEGEMM_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
   return MOEGEMM_OK;
+}
+
+// Preconditions of the LDS-DMA fast path for one problem (see gemm_fast.h).
+bool vector_layout_ok(const void* a, const void* b, const void* c, int64_t m, int64_t n, int64_t k, int64_t sam,
+                      int64_t sak, int64_t sbk, int64_t sbn, int64_t scm, int64_t scn, int dtype) {
+  if (dtype != DT_BF16 && dtype != DT_F16) return false;
+  if (sak != 1 || sbn != 1 || scn != 1) return false;
+  if (k % 8 || n % 8 || sam % 8 || sbk % 8 || scm % 4 || sam < k || sbk < n || scm < n) return false;
+  if ((reinterpret_cast<uintptr_t>(a) & 15) || (reinterpret_cast<uintptr_t>(b) & 15) ||
+      (reinterpret_cast<uintptr_t>(c) & 7))
+    return false;
+  const int64_t limit = int64_t(1) << 31;
+  return (m * sam * 2 < limit) && (k * sbk * 2 < limit);
 }
 
 }  // namespace
@@ -109,7 +123,7 @@ int moegemm_grouped_gemm(const int64_t* a_ptrs, const int64_t* b_ptrs, const int
                          const int64_t* strides, int32_t problem_count, int32_t m, int32_t n, int32_t k,
                          int32_t homogeneous, int32_t total_tiles, int32_t dtype, int32_t input_precision,
                          int32_t block_m, int32_t block_n, int32_t block_k, int32_t group_size_m, int32_t num_warps,
-                         int32_t num_stages, int32_t grid_size, void* stream) {
+                         int32_t num_stages, int32_t grid_size, int32_t vector_layout, void* stream) {
   const KernelEntry* e = nullptr;
   int rc = check_common(dtype, input_precision, group_size_m, &e, block_m, block_n, block_k, num_warps, num_stages);
   if (rc != MOEGEMM_OK) return rc;
@@ -143,7 +157,7 @@ int moegemm_grouped_gemm(const int64_t* a_ptrs, const int64_t* b_ptrs, const int
   }
   if (p.total_tiles == 0) return MOEGEMM_OK;
   int grid = grid_size <= 0 ? p.total_tiles : (grid_size < p.total_tiles ? grid_size : p.total_tiles);
-  return launch(e, p, grid, stream);
+  return launch(e, p, grid, vector_layout != 0, stream);
 }
 
 int moegemm_matmul(const void* a, const void* b, void* c, int32_t m, int32_t n, int32_t k, int64_t stride_am,
@@ -177,7 +191,8 @@ int moegemm_matmul(const void* a, const void* b, void* c, int32_t m, int32_t n, 
   p.tf32 = input_precision == MOEGEMM_PRECISION_TF32;
   p.total_tiles = (int32_t)tiles;
   int grid = grid_size <= 0 ? p.total_tiles : (grid_size < p.total_tiles ? grid_size : p.total_tiles);
-  return launch(e, p, grid, stream);
+  return launch(e, p, grid, vector_layout_ok(a, b, c, m, n, k, stride_am, stride_ak, stride_bk, stride_bn, stride_cm,
+                                           stride_cn, dtype), stream);
 }
 
 }  // extern "C"

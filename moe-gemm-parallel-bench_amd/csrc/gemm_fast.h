@@ -1,0 +1,325 @@
+// Fast path of the grouped GEMM for 16-bit operands in vector layouts (gfx950).
+//
+// Same tile semantics, LDS layout and MFMA fragment reads as GemmTile (gemm_kernel.h); what
+// differs is how K slices reach LDS:
+//  * Each tile builds two buffer resources: the A row panel (num_records = valid rows * row
+//    pitch) and the B column panel (base at column n0, num_records up to the end of B).  Rows past
+//    M or K fall outside the range and chunks past K (A) or N (B) get an out-of-range offset, so
+//    the hardware writes zeros into LDS for every tail element: no branches, no per-element masks.
+//  * K slices are copied global -> LDS by buffer_load_dwordx4 ... lds (no VGPR staging).  One
+//    wave instruction moves 1 KiB: lane l's 16 bytes land at M0 + 16*l, so each lane fetches the
+//    global chunk that the XOR swizzle assigns to its LDS slot.
+//  * STAGES LDS buffers form a ring; STAGES-1 slices are in flight while the MFMAs consume the
+//    current one.  The compiler does not track LDS-DMA completion, so the loop waits explicitly:
+//    s_waitcnt vmcnt(<loads issued after the current slice>) then s_barrier (each wave has seen
+//    its own copies land; the barrier makes that true for all waves).  The slice refilled after
+//    the barrier is the one every wave finished reading in the previous iteration, so one
+//    barrier per K slice suffices.  Compiler memory barriers keep LDS reads from moving across.
+//  * Fragment reads for K step kk+1 are issued before the MFMAs of step kk (register double
+//    buffering) so the MFMA pipe does not wait on LDS latency inside a slice.
+// Preconditions (checked by the host before choosing this variant): fp16/bf16, unit inner strides,
+// row pitches and the K, N extents multiples of 8 elements, every matrix < 2 GiB.
+#pragma once
+
+#include "gemm_kernel.h"
+
+namespace moegemm {
+
+// Raw buffer resource word 3 for gfx9 untyped buffer loads (32-bit data format).
+constexpr uint32_t kBufferFlags = 0x00020000u;
+constexpr uint32_t kOutOfRange = 0x80000000u;
+
+#define MOEGEMM_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
+
+__device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt field is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <class E, int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_>
+struct FastTile {
+  static_assert(!E::is_f32, "the DMA fast path is for 16-bit operands");
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, STAGES = STAGES_;
+  static constexpr int NW = WM * WN;
+  static constexpr int NT = NW * 64;
+  static constexpr int WTM = BM / WM;
+  static constexpr int WTN = BN / WN;
+  static constexpr int MI = (WTM >= 32 && WTN >= 32) ? 32 : 16;
+  static constexpr int MIK = MI == 32 ? 16 : 32;
+  static constexpr int KK = BK / MIK;
+  static constexpr int FM = WTM / MI;
+  static constexpr int FN = WTN / MI;
+  static constexpr int ACC = MI * MI / 64;
+  static constexpr int CA = BK / 8;  // 16-byte chunks per A row
+  static constexpr int CB = BN / 8;  // 16-byte chunks per B row
+  static constexpr int A_BYTES = BM * BK * 2;
+  static constexpr int B_BYTES = BK * BN * 2;
+  static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+  static constexpr int IA = A_BYTES / 1024;  // 1 KiB DMA issues per stage
+  static constexpr int IB = B_BYTES / 1024;
+  static constexpr int QA = (IA + NW - 1) / NW;  // A issues per wave (upper bound)
+  static constexpr int QB = (IB + NW - 1) / NW;
+  static constexpr int XMIN = IA / NW + IB / NW;  // issues per stage every wave makes
+  static constexpr int RPA = 64 / CA;             // A rows per issue
+  static constexpr int RPB = 64 / CB;             // B rows per issue
+  static constexpr int PREFIX = 512;
+  static constexpr int PREFIX_OFFSET = STAGES * STAGE_BYTES;
+  static constexpr int LDS_BYTES = PREFIX_OFFSET + (PREFIX + 1) * 4 + NT * 4;
+
+  static_assert(STAGES >= 2, "need at least double buffering");
+  static_assert(A_BYTES % 1024 == 0 && B_BYTES % 1024 == 0, "stages must be whole 1 KiB DMA issues");
+  static_assert(CA <= 64 && CB <= 64 && 64 % CA == 0 && 64 % CB == 0, "rows must tile a 1 KiB issue");
+  static_assert(CB >= 4, "transpose reads need at least 32 columns");
+  static_assert(WTM % MI == 0 && WTN % MI == 0 && BK % MIK == 0, "tile shape");
+  static_assert((STAGES - 2) * XMIN < 64, "vmcnt budget");
+  static_assert(LDS_BYTES <= 160 * 1024, "LDS budget of one CU");
+
+  using acc_t = typename std::conditional<ACC == 16, f32x16_t, f32x4_t>::type;
+
+  struct Dma {
+    __amdgpu_buffer_rsrc_t ra, rb;
+    uint32_t a_off[QA];  // byte offset at k0 = 0, or kOutOfRange
+    uint32_t a_kch[QA];  // k index of the lane's chunk at k0 = 0
+    uint32_t b_off[QB];
+    int32_t k;
+    uint32_t ldb_bytes;
+  };
+
+  __device__ static __forceinline__ void setup_dma(Dma& d, const ProblemDesc& pd, int m0, int n0) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t lda_bytes = (uint32_t)pd.sam * 2u;
+    d.ldb_bytes = (uint32_t)pd.sbk * 2u;
+    d.k = pd.k;
+    const int rows = min(BM, pd.m - m0);
+    d.ra = __builtin_amdgcn_make_buffer_rsrc((void*)(pd.a + (int64_t)m0 * lda_bytes), 0,
+                                             (int)((uint32_t)rows * lda_bytes), kBufferFlags);
+    d.rb = __builtin_amdgcn_make_buffer_rsrc((void*)(pd.b + (int64_t)n0 * 2), 0,
+                                             (int)((uint32_t)pd.k * d.ldb_bytes - (uint32_t)n0 * 2u), kBufferFlags);
+#pragma unroll
+    for (int q = 0; q < QA; ++q) {
+      const int j = wave + q * NW;
+      const int r = j * RPA + lane / CA;
+      const int pc = lane % CA;
+      const int c = pc ^ swz_a(r, CA);
+      d.a_kch[q] = (uint32_t)(c * 8);
+      d.a_off[q] = (uint32_t)r * lda_bytes + (uint32_t)c * 16u;
+    }
+#pragma unroll
+    for (int q = 0; q < QB; ++q) {
+      const int j = wave + q * NW;
+      const int r = j * RPB + lane / CB;
+      const int pc = lane % CB;
+      const int c = pc ^ swz_b(r, CB);
+      d.b_off[q] = (n0 + c * 8 < pd.n) ? (uint32_t)r * d.ldb_bytes + (uint32_t)c * 16u : kOutOfRange;
+    }
+  }
+
+  // Copy K slice [k0, k0 + BK) into LDS stage `stage`.
+  __device__ static __forceinline__ void issue_stage(const Dma& d, char* smem, int stage, int k0) {
+    const int wave = threadIdx.x >> 6;
+    char* base = smem + stage * STAGE_BYTES;
+#pragma unroll
+    for (int q = 0; q < QA; ++q) {
+      const int j = wave + q * NW;
+      if (IA % NW == 0 || j < IA) {
+        const uint32_t off = ((int)d.a_kch[q] + k0 < d.k) ? d.a_off[q] + (uint32_t)k0 * 2u : kOutOfRange;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(d.ra, MOEGEMM_LDS_PTR(base + j * 1024), 16, off, 0, 0, 0);
+      }
+    }
+    const uint32_t kstep = (uint32_t)k0 * d.ldb_bytes;
+#pragma unroll
+    for (int q = 0; q < QB; ++q) {
+      const int j = wave + q * NW;
+      if (IB % NW == 0 || j < IB) {
+        const uint32_t off = d.b_off[q] == kOutOfRange ? kOutOfRange : d.b_off[q] + kstep;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(d.rb, MOEGEMM_LDS_PTR(base + A_BYTES + j * 1024), 16, off, 0, 0,
+                                                 0);
+      }
+    }
+  }
+
+  __device__ static __forceinline__ void load_frags(i16x8_t (&af)[FM], i16x8_t (&bf)[FN], const char* lds_a,
+                                                    const char* lds_b, int kk, int wave_m, int wave_n) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      const int row = wave_m * WTM + fm * MI + (lane % MI);
+      const int c = (kk * MIK) / 8 + lane / MI;
+      const int pc = c ^ swz_a(row, CA);
+      af[fm] = *reinterpret_cast<const i16x8_t*>(lds_a + (row * CA + pc) * 16);
+    }
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) {
+      const int g = lane >> 4, s = lane & 15;
+      int row, col;
+      if constexpr (MI == 32) {
+        row = kk * MIK + 8 * (g >> 1) + (s >> 2);
+        col = wave_n * WTN + fn * 32 + 16 * (g & 1) + 4 * (s & 3);
+      } else {
+        row = kk * MIK + 8 * g + (s >> 2);
+        col = wave_n * WTN + fn * 16 + 4 * (s & 3);
+      }
+      const int pc = (col >> 3) ^ swz_b(row, CB);
+      const char* p0 = lds_b + (row * CB + pc) * 16 + (col & 7) * 2;
+      const char* p1 = p0 + 4 * CB * 16;
+      i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)(p0));
+      i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)(p1));
+      bf[fn] = i16x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+  }
+
+  __device__ static __forceinline__ void mfmas(acc_t (&acc)[FM][FN], const i16x8_t (&af)[FM], const i16x8_t (&bf)[FN]) {
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) {
+        if constexpr (E::dtype == DT_BF16) {
+          if constexpr (MI == 32)
+            acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                __builtin_bit_cast(bf16x8_t, bf[fn]), __builtin_bit_cast(bf16x8_t, af[fm]), acc[fm][fn], 0, 0, 0);
+          else
+            acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(bf16x8_t, bf[fn]), __builtin_bit_cast(bf16x8_t, af[fm]), acc[fm][fn], 0, 0, 0);
+        } else {
+          if constexpr (MI == 32)
+            acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                __builtin_bit_cast(f16x8_t, bf[fn]), __builtin_bit_cast(f16x8_t, af[fm]), acc[fm][fn], 0, 0, 0);
+          else
+            acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                __builtin_bit_cast(f16x8_t, bf[fn]), __builtin_bit_cast(f16x8_t, af[fm]), acc[fm][fn], 0, 0, 0);
+        }
+      }
+  }
+
+  // MFMAs of fragment columns [fm0, fm1) of one K step.
+  template <int FM0, int FM1>
+  __device__ static __forceinline__ void mfma_rows(acc_t (&acc)[FM][FN], const i16x8_t (&af)[FM],
+                                                   const i16x8_t (&bf)[FN]) {
+#pragma unroll
+    for (int fm = FM0; fm < FM1; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) {
+        if constexpr (E::dtype == DT_BF16) {
+          if constexpr (MI == 32)
+            acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                __builtin_bit_cast(bf16x8_t, bf[fn]), __builtin_bit_cast(bf16x8_t, af[fm]), acc[fm][fn], 0, 0, 0);
+          else
+            acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(bf16x8_t, bf[fn]), __builtin_bit_cast(bf16x8_t, af[fm]), acc[fm][fn], 0, 0, 0);
+        } else {
+          if constexpr (MI == 32)
+            acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                __builtin_bit_cast(f16x8_t, bf[fn]), __builtin_bit_cast(f16x8_t, af[fm]), acc[fm][fn], 0, 0, 0);
+          else
+            acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                __builtin_bit_cast(f16x8_t, bf[fn]), __builtin_bit_cast(f16x8_t, af[fm]), acc[fm][fn], 0, 0, 0);
+        }
+      }
+  }
+
+  // Scheduling hints: interleave `mfma` MFMAs with `ds` LDS reads and `vm` DMA issues.
+  template <int NMFMA, int NDS, int NVM>
+  __device__ static __forceinline__ void interleave() {
+    constexpr int vm_per = NMFMA > 0 ? (NVM + NMFMA - 1) / NMFMA : 0;
+    constexpr int ds_per = NMFMA > 0 ? (NDS + NMFMA - 1) / NMFMA : 0;
+#pragma unroll
+    for (int i = 0; i < NMFMA; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      if constexpr (vm_per > 0) __builtin_amdgcn_sched_group_barrier(0x020, vm_per, 0);  // VMEM reads
+      if constexpr (ds_per > 0) __builtin_amdgcn_sched_group_barrier(0x100, ds_per, 0);  // LDS reads
+    }
+  }
+
+  __device__ static __forceinline__ void store_tile(const acc_t (&acc)[FM][FN], const ProblemDesc& pd, int m0,
+                                                    int n0, int wave_m, int wave_n) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      const int gm = m0 + wave_m * WTM + fm * MI + (lane % MI);
+      if (gm >= pd.m) continue;
+      char* crow = pd.c + (int64_t)gm * pd.scm * 2;
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) {
+#pragma unroll
+        for (int q = 0; q < ACC / 4; ++q) {
+          const int nloc = (MI == 32) ? (q * 8 + (lane >> 5) * 4) : ((lane >> 4) * 4);
+          const int gn = n0 + wave_n * WTN + fn * MI + nloc;
+          if (gn < pd.n) {
+            f32x4_t v = {acc[fm][fn][q * 4 + 0], acc[fm][fn][q * 4 + 1], acc[fm][fn][q * 4 + 2],
+                         acc[fm][fn][q * 4 + 3]};
+            store4<E>(crow + (int64_t)gn * 2, v);
+          }
+        }
+      }
+    }
+  }
+
+  __device__ static __forceinline__ void run_tile(const ProblemDesc& pd, int tm, int tn, char* smem, bool) {
+    static_assert(KK % 2 == 0, "fragment double buffer alternates by K step");
+    constexpr int HALF = FM / 2 > 0 ? FM / 2 : 1;  // fragment rows issued before the mid-slice barrier
+    constexpr int NDS = FM + 2 * FN;                 // LDS reads per K step
+    constexpr int NVM = QA + QB;                      // DMA issues per slice (upper bound per wave)
+    const int wave = threadIdx.x >> 6;
+    const int wave_m = wave / WN, wave_n = wave % WN;
+    const int m0 = tm * BM, n0 = tn * BN;
+    Dma d;
+    setup_dma(d, pd, m0, n0);
+
+    acc_t acc[FM][FN];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int i = 0; i < ACC; ++i) acc[fm][fn][i] = 0.0f;
+
+    // Prologue: slices 0..STAGES-1 in flight, then slice 0 resident and its first fragments read.
+    // Slices at or past K read out of range and land as zeros, so every copy is unconditional.
+#pragma unroll
+    for (int s = 0; s < STAGES; ++s) issue_stage(d, smem, s, s * BK);
+    wait_vmcnt<(STAGES - 1) * XMIN>();
+    compiler_fence();
+    __builtin_amdgcn_s_barrier();
+    compiler_fence();
+    i16x8_t af[2][FM], bf[2][FN];
+    load_frags(af[0], bf[0], smem, smem + A_BYTES, 0, wave_m, wave_n);
+
+    const int kt_count = (pd.k + BK - 1) / BK;
+    for (int kt = 0; kt < kt_count; ++kt) {
+      const char* cur = smem + (kt % STAGES) * STAGE_BYTES;
+      const char* nxt = smem + ((kt + 1) % STAGES) * STAGE_BYTES;
+#pragma unroll
+      for (int kk = 0; kk < KK - 1; ++kk) {
+        load_frags(af[(kk + 1) & 1], bf[(kk + 1) & 1], cur, cur + A_BYTES, kk + 1, wave_m, wave_n);
+        mfma_rows<0, FM>(acc, af[kk & 1], bf[kk & 1]);
+        interleave<FM * FN, NDS, 0>();
+      }
+      constexpr int L = (KK - 1) & 1;
+      // Last K step: first half of its MFMAs, then slice kt+1 becomes readable (this wave's copies
+      // landed, then every wave's), the drained buffer of slice kt is refilled with slice
+      // kt+STAGES, and slice kt+1's first fragments load under the second half of the MFMAs.
+      mfma_rows<0, HALF>(acc, af[L], bf[L]);
+      wait_vmcnt<(STAGES - 2) * XMIN>();
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      compiler_fence();
+      __builtin_amdgcn_s_barrier();
+      compiler_fence();
+      issue_stage(d, smem, kt % STAGES, (kt + STAGES) * BK);
+      load_frags(af[0], bf[0], nxt, nxt + A_BYTES, 0, wave_m, wave_n);
+      mfma_rows<HALF, FM>(acc, af[L], bf[L]);
+      interleave<(FM - HALF) * FN, NDS, NVM>();
+    }
+    // All copies (including the out-of-range tail slices) landed and every wave is done reading
+    // LDS before the next tile's prologue refills it.
+    wait_vmcnt<0>();
+    compiler_fence();
+    __builtin_amdgcn_s_barrier();
+    compiler_fence();
+    store_tile(acc, pd, m0, n0, wave_m, wave_n);
+  }
+};
+
+}  // namespace moegemm

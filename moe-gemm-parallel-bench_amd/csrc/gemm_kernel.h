@@ -71,6 +71,34 @@ struct ProblemDesc {
   int64_t sam, sak, sbk, sbn, scm, scn;
 };
 
+// Wave-uniform copies: values derived from LDS (the generic-mode prefix search) are treated as
+// divergent by the compiler; reading lane 0 makes every descriptor scalar again, so table loads
+// become scalar loads and buffer resources need no waterfall loops.
+__device__ __forceinline__ int32_t uniform(int32_t x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ __forceinline__ int64_t uniform(int64_t x) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)(uint64_t)x);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)x >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+template <class P>
+__device__ __forceinline__ P* uniform(P* x) {
+  return reinterpret_cast<P*>(uniform(reinterpret_cast<int64_t>(x)));
+}
+__device__ __forceinline__ void make_uniform(ProblemDesc& pd) {
+  pd.a = uniform(pd.a);
+  pd.b = uniform(pd.b);
+  pd.c = uniform(pd.c);
+  pd.m = uniform(pd.m);
+  pd.n = uniform(pd.n);
+  pd.k = uniform(pd.k);
+  pd.sam = uniform(pd.sam);
+  pd.sak = uniform(pd.sak);
+  pd.sbk = uniform(pd.sbk);
+  pd.sbn = uniform(pd.sbn);
+  pd.scm = uniform(pd.scm);
+  pd.scn = uniform(pd.scn);
+}
+
 // ---------------------------------------------------------------------------------------------
 // Element traits
 struct EBf16 {
@@ -98,23 +126,24 @@ __device__ __forceinline__ uint32_t tf32_round(uint32_t u) {
 template <class E>
 __device__ __forceinline__ void store4(char* dst, f32x4_t v);
 
+#define MOEGEMM_GLOBAL(T, p) ((__attribute__((address_space(1))) T*)(p))
 template <>
 __device__ __forceinline__ void store4<EBf16>(char* dst, f32x4_t v) {
   typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
   bf16x4_t o;
   o[0] = (__bf16)v[0]; o[1] = (__bf16)v[1]; o[2] = (__bf16)v[2]; o[3] = (__bf16)v[3];
-  *reinterpret_cast<bf16x4_t*>(dst) = o;
+  *MOEGEMM_GLOBAL(bf16x4_t, dst) = o;
 }
 template <>
 __device__ __forceinline__ void store4<EF16>(char* dst, f32x4_t v) {
   typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
   f16x4_t o;
   o[0] = (_Float16)v[0]; o[1] = (_Float16)v[1]; o[2] = (_Float16)v[2]; o[3] = (_Float16)v[3];
-  *reinterpret_cast<f16x4_t*>(dst) = o;
+  *MOEGEMM_GLOBAL(f16x4_t, dst) = o;
 }
 template <>
 __device__ __forceinline__ void store4<EF32>(char* dst, f32x4_t v) {
-  *reinterpret_cast<f32x4_t*>(dst) = v;
+  *MOEGEMM_GLOBAL(f32x4_t, dst) = v;
 }
 
 template <class E>
@@ -168,7 +197,8 @@ struct GemmTile {
   static constexpr int B_BYTES = BK * BN * ES;
   static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
   static constexpr int PREFIX = 1024;  // problems per prefix-sum chunk (generic mode)
-  static constexpr int LDS_BYTES = 2 * STAGE_BYTES + (PREFIX + 1) * 4 + NT * 4;
+  static constexpr int PREFIX_OFFSET = 2 * STAGE_BYTES;
+  static constexpr int LDS_BYTES = PREFIX_OFFSET + (PREFIX + 1) * 4 + NT * 4;
 
   static_assert(BM % WM == 0 && BN % WN == 0, "tile must split evenly over waves");
   static_assert(WTM % MI == 0 && WTN % MI == 0, "wave tile must be a multiple of the MFMA tile");
@@ -482,7 +512,7 @@ __device__ __forceinline__ void load_prefix(const KParams& p, int* s_pref, int* 
 template <class T>
 __global__ void __launch_bounds__(T::NT) grouped_gemm_kernel(KParams p) {
   __shared__ __attribute__((aligned(16))) char smem[T::LDS_BYTES];
-  int* s_pref = reinterpret_cast<int*>(smem + 2 * T::STAGE_BYTES);
+  int* s_pref = reinterpret_cast<int*>(smem + T::PREFIX_OFFSET);
   int* s_tot = s_pref + T::PREFIX + 1;
 
   const int grid = gridDim.x;
@@ -527,8 +557,8 @@ __global__ void __launch_bounds__(T::NT) grouped_gemm_kernel(KParams p) {
         const int mid = (lo + hi) >> 1;
         if (s_pref[mid] <= t) lo = mid; else hi = mid;
       }
-      const int e = chunk_first + lo;
-      const int local = t - s_pref[lo];
+      const int e = uniform(chunk_first + lo);
+      const int local = uniform(t - s_pref[lo]);
       pd.m = p.dims[e * 3 + 0]; pd.n = p.dims[e * 3 + 1]; pd.k = p.dims[e * 3 + 2];
       const int mt = (pd.m + T::BM - 1) / T::BM, nt = (pd.n + T::BN - 1) / T::BN;
       group_m_order(local, mt, nt, p.group_m, tm, tn);
@@ -538,7 +568,8 @@ __global__ void __launch_bounds__(T::NT) grouped_gemm_kernel(KParams p) {
       pd.b = reinterpret_cast<const char*>(p.b_ptrs[e]);
       pd.c = reinterpret_cast<char*>(p.c_ptrs[e]);
     }
-    T::run_tile(pd, tm, tn, smem, p.tf32 != 0);
+    make_uniform(pd);
+    T::run_tile(pd, uniform(tm), uniform(tn), smem, p.tf32 != 0);
   }
 }
 

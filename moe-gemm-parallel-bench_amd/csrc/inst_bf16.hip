@@ -1,9 +1,9 @@
 // Compiled bf16 tile configurations.
 #include "registry.h"
 namespace moegemm {
-MOEGEMM_MENU_16BIT(MOEGEMM_INST, EBf16)
+MOEGEMM_MENU_16BIT(MOEGEMM_INST16, EBf16)
 #if !defined(__HIP_DEVICE_COMPILE__)
-const KernelEntry kEntriesBf16[] = {MOEGEMM_MENU_16BIT(MOEGEMM_ENTRY, EBf16)};
+const KernelEntry kEntriesBf16[] = {MOEGEMM_MENU_16BIT(MOEGEMM_ENTRY16, EBf16)};
 const int kNumBf16 = sizeof(kEntriesBf16) / sizeof(kEntriesBf16[0]);
 #endif
 }  // namespace moegemm

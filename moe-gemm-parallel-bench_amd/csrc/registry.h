@@ -1,18 +1,25 @@
-// Table of compiled kernel instantiations.  Each entry is one tile configuration for one dtype.
+// Table of compiled kernel instantiations.  Each entry is one tile configuration for one dtype,
+// with up to two kernels: the LDS-DMA fast path (16-bit operands in vector layouts) and the
+// general register-staged kernel (any strides/alignment, and all fp32 work).
 #pragma once
 #include <hip/hip_runtime.h>
+
+#include "gemm_fast.h"
 #include "gemm_kernel.h"
 
 namespace moegemm {
+
+typedef hipError_t (*LaunchFn)(const KParams&, int grid, hipStream_t stream);
 
 struct KernelEntry {
   int dtype;
   int block_m, block_n, block_k;
   int num_warps;   // wave64 wavefronts per workgroup
-  int num_stages;  // LDS pipeline stages
+  int num_stages;  // LDS stages of the fast path's K pipeline
   int waves_m, waves_n;
-  int lds_bytes;
-  hipError_t (*launch)(const KParams&, int grid, hipStream_t stream);
+  int lds_bytes;   // fast path if present, else general
+  LaunchFn launch_fast;     // null when the dtype has no fast path
+  LaunchFn launch_general;
 };
 
 template <class T>
@@ -21,27 +28,41 @@ hipError_t launch_tile(const KParams& p, int grid, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// X-macro menus: X(E, BM, BN, BK, WAVES_M, WAVES_N).  Each translation unit expands a menu twice:
-// once into explicit kernel instantiations (device and host passes) and once into the host-side
-// launch table.
-#define MOEGEMM_INST(E, BM, BN, BK, WM, WN) \
-  template __global__ void grouped_gemm_kernel<GemmTile<E, BM, BN, BK, WM, WN>>(KParams);
-#define MOEGEMM_ENTRY(E, BM, BN, BK, WM, WN)                                                  \
-  KernelEntry{E::dtype, BM, BN, BK, (WM) * (WN), 2, WM, WN,                                   \
-              GemmTile<E, BM, BN, BK, WM, WN>::LDS_BYTES, &launch_tile<GemmTile<E, BM, BN, BK, WM, WN>>},
+// X-macro menus: X(E, BM, BN, BK, WAVES_M, WAVES_N, STAGES).  Each translation unit expands a
+// menu into explicit kernel instantiations (device and host passes) and into the host table.
+#define MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S) FastTile<E, BM, BN, BK, WM, WN, S>
+#define MOEGEMM_GEN(E, BM, BN, BK, WM, WN) GemmTile<E, BM, BN, BK, WM, WN>
+
+#define MOEGEMM_INST16(E, BM, BN, BK, WM, WN, S)                                              \
+  template __global__ void grouped_gemm_kernel<MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S)>(KParams); \
+  template __global__ void grouped_gemm_kernel<MOEGEMM_GEN(E, BM, BN, BK, WM, WN)>(KParams);
+#define MOEGEMM_ENTRY16(E, BM, BN, BK, WM, WN, S)                                             \
+  KernelEntry{E::dtype, BM, BN, BK, (WM) * (WN), S, WM, WN,                                   \
+              MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S)::LDS_BYTES,                              \
+              &launch_tile<MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S)>,                          \
+              &launch_tile<MOEGEMM_GEN(E, BM, BN, BK, WM, WN)>},
+
+#define MOEGEMM_INST32(E, BM, BN, BK, WM, WN, S) \
+  template __global__ void grouped_gemm_kernel<MOEGEMM_GEN(E, BM, BN, BK, WM, WN)>(KParams);
+#define MOEGEMM_ENTRY32(E, BM, BN, BK, WM, WN, S)                                             \
+  KernelEntry{E::dtype, BM, BN, BK, (WM) * (WN), S, WM, WN,                                   \
+              MOEGEMM_GEN(E, BM, BN, BK, WM, WN)::LDS_BYTES, nullptr,                         \
+              &launch_tile<MOEGEMM_GEN(E, BM, BN, BK, WM, WN)>},
 
 // 16-bit menu (bf16 and f16 share it): large-M MFMA-bound tiles down to skinny-M streaming tiles.
+// STAGES is sized to the 160 KiB LDS of a CU.
 #define MOEGEMM_MENU_16BIT(X, E)                                                             \
-  X(E, 256, 256, 64, 2, 2) X(E, 256, 128, 64, 2, 2) X(E, 128, 256, 64, 2, 2)                 \
-  X(E, 128, 128, 64, 2, 2) X(E, 128, 64, 64, 2, 2) X(E, 64, 256, 64, 1, 4)                   \
-  X(E, 64, 128, 64, 2, 2) X(E, 64, 64, 64, 2, 2) X(E, 64, 64, 32, 2, 2)                      \
-  X(E, 32, 256, 64, 1, 4) X(E, 32, 128, 64, 1, 4) X(E, 32, 128, 128, 1, 4)                   \
-  X(E, 16, 256, 64, 1, 4) X(E, 16, 256, 128, 1, 4) X(E, 16, 128, 128, 1, 4)                  \
-  X(E, 16, 64, 128, 1, 4)
+  X(E, 256, 256, 64, 2, 2, 2) X(E, 256, 256, 32, 2, 2, 4) X(E, 256, 128, 64, 2, 2, 3)        \
+  X(E, 128, 256, 64, 2, 2, 3) X(E, 128, 128, 64, 2, 2, 4) X(E, 128, 64, 64, 2, 2, 4)         \
+  X(E, 64, 256, 64, 1, 4, 3) X(E, 64, 128, 64, 2, 2, 4) X(E, 64, 64, 64, 2, 2, 4)            \
+  X(E, 32, 256, 64, 1, 4, 4) X(E, 32, 128, 64, 1, 4, 4) X(E, 32, 128, 128, 1, 4, 3)          \
+  X(E, 16, 256, 64, 1, 4, 4) X(E, 16, 256, 128, 1, 4, 2) X(E, 16, 128, 128, 1, 4, 4)         \
+  X(E, 16, 64, 128, 1, 4, 4)
 
+// fp32 menu (general kernel, v_mfma_f32_16x16x4_f32); STAGES is the register-staged double buffer.
 #define MOEGEMM_MENU_F32(X, E)                                                               \
-  X(E, 128, 128, 32, 2, 2) X(E, 64, 64, 32, 2, 2) X(E, 32, 64, 32, 1, 4)                     \
-  X(E, 16, 64, 32, 1, 4) X(E, 32, 32, 32, 1, 2)
+  X(E, 128, 128, 32, 2, 2, 2) X(E, 64, 64, 32, 2, 2, 2) X(E, 32, 64, 32, 1, 4, 2)            \
+  X(E, 16, 64, 32, 1, 4, 2) X(E, 32, 32, 32, 1, 2, 2)
 
 extern const KernelEntry kEntriesBf16[];
 extern const int kNumBf16;

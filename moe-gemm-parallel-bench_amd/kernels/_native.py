@@ -15,7 +15,7 @@ from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().with_name("libmoegemm.so")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 OK = 0
 ERR_INVALID = -1
 ERR_NO_KERNEL = -2
@@ -42,7 +42,7 @@ SIGNATURES = {
     "moegemm_grouped_gemm": (
         ctypes.c_int,
         [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
-         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
+         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
     ),
     "moegemm_matmul": (
         ctypes.c_int,

@@ -266,6 +266,38 @@ def _grid_size(workspace: GroupedWorkspace, config: KernelConfig) -> int:
     return max(1, min(tiles, workspace.sm_count * config.cta_multiplier))
 
 
+_TWO_GIB = 1 << 31
+
+
+def _problem_vector_ok(a, b, c) -> bool:
+    """Preconditions of the LDS-DMA kernel for one problem (see include/moegemm.h)."""
+    m, k = a.shape
+    n = b.shape[1]
+    sam, sak = a.stride()
+    sbk, sbn = b.stride()
+    scm, scn = c.stride()
+    return (
+        sak == 1 and sbn == 1 and scn == 1
+        and k % 8 == 0 and n % 8 == 0 and sam % 8 == 0 and sbk % 8 == 0 and scm % 4 == 0
+        and sam >= k and sbk >= n and scm >= n
+        and a.data_ptr() % 16 == 0 and b.data_ptr() % 16 == 0 and c.data_ptr() % 8 == 0
+        and m * sam * 2 < _TWO_GIB and k * sbk * 2 < _TWO_GIB
+    )
+
+
+def _vector_layout(workspace: GroupedWorkspace, dtype_code: int) -> bool:
+    """True when every problem meets the fast kernel's layout; cached per set of tensor objects."""
+    if dtype_code == _native.DTYPE_F32:
+        return False
+    key = (tuple(map(id, workspace.a)), tuple(map(id, workspace.b)), tuple(map(id, workspace.c)))
+    cached = getattr(workspace, "_layout_cache", None)
+    if cached is not None and cached[0] == key:
+        return cached[1]
+    value = all(_problem_vector_ok(a, b, c) for a, b, c in zip(workspace.a, workspace.b, workspace.c))
+    workspace._layout_cache = (key, value)
+    return value
+
+
 def _check_workspace(workspace: GroupedWorkspace) -> int:
     a0, b0, c0 = workspace.a[0], workspace.b[0], workspace.c[0]
     if a0.device.type != "cuda":
@@ -284,7 +316,8 @@ def _launch_grouped_fixed(workspace: GroupedWorkspace, cfg: KernelConfig, dtype_
         workspace.problem_count, m, n, k, 1 if workspace.homogeneous else 0,
         workspace.tile_count_for(cfg), dtype_code, precision,
         cfg.block_m, cfg.block_n, cfg.block_k, cfg.group_size_m, cfg.num_warps, cfg.num_stages,
-        _grid_size(workspace, cfg), _native.current_stream_handle(workspace.a[0].device),
+        _grid_size(workspace, cfg), 1 if _vector_layout(workspace, dtype_code) else 0,
+        _native.current_stream_handle(workspace.a[0].device),
     )
     _native.check(status)
 

@@ -47,12 +47,12 @@ class KernelConfig:
 # Compiled tile menus: (block_m, block_n, block_k, num_warps, num_stages).  They must equal the
 # X-macro menus of csrc/registry.h; tests/test_native_abi.py compares them with the library.
 _MENU_16BIT: tuple[tuple[int, int, int, int, int], ...] = (
-    (256, 256, 64, 4, 2), (256, 128, 64, 4, 2), (128, 256, 64, 4, 2),
-    (128, 128, 64, 4, 2), (128, 64, 64, 4, 2), (64, 256, 64, 4, 2),
-    (64, 128, 64, 4, 2), (64, 64, 64, 4, 2), (64, 64, 32, 4, 2),
-    (32, 256, 64, 4, 2), (32, 128, 64, 4, 2), (32, 128, 128, 4, 2),
-    (16, 256, 64, 4, 2), (16, 256, 128, 4, 2), (16, 128, 128, 4, 2),
-    (16, 64, 128, 4, 2),
+    (256, 256, 64, 4, 2), (256, 256, 32, 4, 4), (256, 128, 64, 4, 3),
+    (128, 256, 64, 4, 3), (128, 128, 64, 4, 4), (128, 64, 64, 4, 4),
+    (64, 256, 64, 4, 3), (64, 128, 64, 4, 4), (64, 64, 64, 4, 4),
+    (32, 256, 64, 4, 4), (32, 128, 64, 4, 4), (32, 128, 128, 4, 3),
+    (16, 256, 64, 4, 4), (16, 256, 128, 4, 2), (16, 128, 128, 4, 4),
+    (16, 64, 128, 4, 4),
 )
 _MENU_F32: tuple[tuple[int, int, int, int, int], ...] = (
     (128, 128, 32, 4, 2), (64, 64, 32, 4, 2), (32, 64, 32, 4, 2),
