@@ -47,8 +47,8 @@ class KernelConfig:
 # Compiled tile menus: (block_m, block_n, block_k, num_warps, num_stages).  They must equal the
 # X-macro menus of csrc/registry.h; tests/test_native_abi.py compares them with the library.
 _MENU_16BIT: tuple[tuple[int, int, int, int, int], ...] = (
-    (256, 256, 64, 4, 2), (256, 256, 32, 4, 4), (256, 128, 64, 4, 3),
-    (128, 256, 64, 4, 3), (128, 128, 64, 4, 4), (128, 64, 64, 4, 4),
+    (256, 256, 64, 8, 2), (256, 256, 64, 4, 2), (256, 256, 32, 4, 4),
+    (256, 128, 64, 4, 3), (128, 256, 64, 8, 3), (128, 256, 64, 4, 3), (128, 128, 64, 4, 4), (128, 64, 64, 4, 4),
     (64, 256, 64, 4, 3), (64, 128, 64, 4, 4), (64, 64, 64, 4, 4),
     (32, 256, 64, 4, 4), (32, 128, 64, 4, 4), (32, 128, 128, 4, 3),
     (16, 256, 64, 4, 4), (16, 256, 128, 4, 2), (16, 128, 128, 4, 4),
@@ -123,26 +123,26 @@ def select_config(m: int, n: int, k: int, dtype=None) -> KernelConfig:
 def diverse_configs(ordered: list[KernelConfig], limit: int) -> list[KernelConfig]:
     """Truncate a best-first list to ``limit`` while covering distinct tile/traversal choices.
 
-    Walks the ranking in order and first takes each config that adds a (block_m, block_n),
-    block_k or group_size_m value not yet selected; remaining slots are filled best-first.
+    Each pick is the remaining config that adds the most not-yet-covered choices, where a new
+    (block_m, block_n) tile counts twice and a new block_k, GROUP_M, wave count or stage count
+    once each; ties go to the better-ranked config.
     """
-    limit = max(1, limit)
-    unique = list(dict.fromkeys(ordered))
+    def novelty(cfg: KernelConfig, seen: set) -> int:
+        score = 2 if ("tile", (cfg.block_m, cfg.block_n)) not in seen else 0
+        for key in (("bk", cfg.block_k), ("group", cfg.group_size_m), ("warps", cfg.num_warps),
+                    ("stages", cfg.num_stages)):
+            score += key not in seen
+        return score
+
+    remaining = list(dict.fromkeys(ordered))
     chosen: list[KernelConfig] = []
-    seen: set[tuple[str, object]] = set()
-    for cfg in unique:
-        if len(chosen) >= limit:
-            break
-        keys = {("tile", (cfg.block_m, cfg.block_n)), ("bk", cfg.block_k), ("group", cfg.group_size_m),
-                ("warps", cfg.num_warps), ("stages", cfg.num_stages)}
-        if keys - seen:
-            chosen.append(cfg)
-            seen |= keys
-    for cfg in unique:
-        if len(chosen) >= limit:
-            break
-        if cfg not in chosen:
-            chosen.append(cfg)
+    seen: set = set()
+    while remaining and len(chosen) < max(1, limit):
+        best = max(range(len(remaining)), key=lambda i: (novelty(remaining[i], seen), -i))
+        cfg = remaining.pop(best)
+        chosen.append(cfg)
+        seen |= {("tile", (cfg.block_m, cfg.block_n)), ("bk", cfg.block_k), ("group", cfg.group_size_m),
+                 ("warps", cfg.num_warps), ("stages", cfg.num_stages)}
     return chosen
 
 

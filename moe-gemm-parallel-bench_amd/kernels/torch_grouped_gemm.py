@@ -71,8 +71,14 @@ def torch_grouped_mm_unavailable_reason(dtype=None, problem_count: int = 1) -> s
 _METADATA_KERNELS = ("prepare_grouped_gemm_data", "fill", "offsets")
 
 
+def _is_metadata(name: str) -> bool:
+    return any(tag in name for tag in _METADATA_KERNELS)
+
+
 def _is_grouped_compute(name: str) -> bool:
     lowered = name.lower()
+    if _is_metadata(lowered):
+        return False
     return "group" in lowered and ("gemm" in lowered or "_mm" in lowered or "matmul" in lowered)
 
 
@@ -88,7 +94,7 @@ def inspect_grouped_trace(cpu_ops: Sequence[str], gpu_events: Sequence[str]) -> 
     kernels = [n for n in names if "memset" not in n]
     compute = [n for n in kernels if _is_grouped_compute(n)]
     others = [n for n in kernels if n not in compute]
-    if len(compute) != 1 or any(not any(tag in n for tag in _METADATA_KERNELS) for n in others):
+    if len(compute) != 1 or any(not _is_metadata(n) for n in others):
         raise TorchGroupedMMUnavailable(f"device trace does not prove one grouped compute kernel: {kernels}")
     return {
         "execution_verified": True,

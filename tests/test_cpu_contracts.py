@@ -1,0 +1,376 @@
+"""Hardware-independent contract tests of the host layer (mirrors the reference's tests/test_cpu.py
+where the contract carries over; Triton-tutorial and plotting checks have no counterpart here)."""
+
+from __future__ import annotations
+
+import json
+import math
+from pathlib import Path
+from types import SimpleNamespace
+from unittest.mock import patch
+
+import pytest
+import torch
+
+from benchmark import main, parser
+from benchmark_moe import _estimate, run_moe
+from kernels.grouped_gemm import (
+    _GROUPED_BASE_CONFIG_POOL,
+    _shape_signature,
+    build_fused_gate_up_workspace,
+    build_grouped_workspace,
+    grouped_candidate_configs,
+    workspace_from_tensors,
+)
+from kernels.matmul import (
+    _MATMUL_CONFIG_POOL,
+    _MATMUL_CONFIG_POOL_F32,
+    KernelConfig,
+    diverse_configs,
+    matmul_candidate_configs,
+    select_config,
+)
+from kernels.torch_grouped_gemm import (
+    TorchGroupedMMUnavailable,
+    build_torch_grouped_workspace,
+    inspect_grouped_trace,
+    launch_torch_grouped,
+)
+from utils.benchmark import _whole_ring_count, percentile, time_cuda
+from utils.config import load_model_defaults
+from utils.io import CSV_FIELDS, read_rows, write_rows
+from utils.metrics import arithmetic_intensity, gemm_flops, moe_shapes, tile_metrics, verify_ep_tp_flops
+from validate_results import (
+    _derivable_metrics_valid,
+    _moe_execution_contract_valid,
+    _projection_contract_valid,
+    validate_results,
+)
+
+CONFIGS = Path(__file__).resolve().parents[1] / "moe-gemm-parallel-bench_amd" / "model_configs"
+
+
+def test_timing_counts_visit_complete_workspace_rings():
+    assert _whole_ring_count(1, 3, 8) == 8
+    assert _whole_ring_count(5, 3, 2) == 6
+    assert _whole_ring_count(100, 3, 1) == 100
+
+
+def test_percentile_interpolates():
+    assert percentile([4.0, 1.0, 3.0, 2.0], 0.5) == 2.5
+    assert percentile([1.0], 0.2) == 1.0
+    assert math.isnan(percentile([], 0.5))
+
+
+def test_time_cuda_rejects_invalid_counts_before_touching_a_gpu():
+    for args in ((0, 1), (-1, 1)):
+        with pytest.raises(ValueError):
+            time_cuda(lambda _: None, args[1], args[0])
+    with pytest.raises(ValueError):
+        time_cuda(lambda _: None, 1, 1, workspace_count=0)
+
+
+def test_deepseek_v3_mapping():
+    config = load_model_defaults(CONFIGS / "deepseek-v3.json")
+    assert (config.hidden_size, config.ffn_size, config.num_experts, config.topk) == (7168, 2048, 256, 8)
+    assert config.dtype == "bf16"
+
+
+def test_all_bundled_model_config_schemas():
+    expected = {
+        "deepseek-v3.json": (7168, 2048, 256, 8), "deepseek-v4-flash.json": (4096, 2048, 256, 6),
+        "glm-5.2.json": (6144, 2048, 256, 8), "gpt-oss-120b.json": (2880, 2880, 128, 4),
+        "kimi-k3.json": (7168, 3072, 896, 16), "llama-4-maverick-17b-128e.json": (5120, 8192, 128, 1),
+        "llama-4-scout-17b-16e.json": (5120, 8192, 16, 1), "mixtral-8x7b.json": (4096, 14336, 8, 2),
+        "qwen3-235b-a22b.json": (4096, 1536, 128, 8), "qwen3-30b-a3b.json": (2048, 768, 128, 8),
+    }
+    for filename, dims in expected.items():
+        config = load_model_defaults(CONFIGS / filename)
+        assert (config.hidden_size, config.ffn_size, config.num_experts, config.topk) == dims, filename
+
+
+def test_config_schema_errors_name_the_missing_field(tmp_path):
+    path = tmp_path / "bad.json"
+    path.write_text(json.dumps({"hidden_size": 8, "num_experts": 4}))
+    with pytest.raises(ValueError, match="ffn_size"):
+        load_model_defaults(path)
+
+
+def test_ep_tp_flops_equal_w1_and_w2():
+    for projection in ("W1", "W2"):
+        total = verify_ep_tp_flops(projection, 17, 7168, 2048, 256, 8)
+        ep = sum(gemm_flops(*s) for s in moe_shapes(projection, "EP", 17, 7168, 2048, 256, 8))
+        tp = sum(gemm_flops(*s) for s in moe_shapes(projection, "TP", 17, 7168, 2048, 256, 8))
+        assert total == ep == tp
+    assert verify_ep_tp_flops("W1", 17, 7168, 2048, 256, 8) == 2 * verify_ep_tp_flops("W2", 17, 7168, 2048, 256, 8)
+
+
+def test_ep_tp_shapes_split_the_intended_dimension():
+    assert moe_shapes("W1", "EP", 17, 7168, 2048, 256, 8) == [(17, 7168, 4096)] * 32
+    assert moe_shapes("W1", "TP", 17, 7168, 2048, 256, 8) == [(17, 7168, 512)] * 256
+    assert moe_shapes("W2", "EP", 17, 7168, 2048, 256, 8) == [(17, 2048, 7168)] * 32
+    assert moe_shapes("W2", "TP", 17, 7168, 2048, 256, 8) == [(17, 256, 7168)] * 256
+
+
+def test_baseline_config_shapes():
+    # Mixtral P=8, Qwen3-30B-A3B P=4.
+    assert moe_shapes("W1", "EP", 16, 4096, 14336, 8, 8) == [(16, 4096, 28672)]
+    assert moe_shapes("W2", "TP", 16, 4096, 14336, 8, 8) == [(16, 1792, 4096)] * 8
+    assert moe_shapes("W1", "TP", 4, 2048, 768, 128, 4) == [(4, 2048, 384)] * 128
+    assert moe_shapes("W2", "EP", 4, 2048, 768, 128, 4) == [(4, 768, 2048)] * 32
+
+
+def test_shape_and_tile_metrics():
+    assert gemm_flops(2, 3, 4) == 48
+    assert arithmetic_intensity(16, 32, 64, 2) == pytest.approx(2 * 16 * 32 * 64 / (2 * (16 * 32 + 32 * 64 + 16 * 64)))
+    metrics = tile_metrics([(17, 31, 65)] * 3, 16, 64, 32, 30)
+    assert metrics["total_output_tiles_per_rank"] == 12
+    assert metrics["estimated_waves"] == 1
+    assert metrics["dot_tiles"] == 12
+    assert 0 < metrics["tile_efficiency"] < 1
+
+
+def test_divisibility_rejected():
+    with pytest.raises(ValueError):
+        moe_shapes("W1", "TP", 1, 8, 10, 8, 4)
+    with pytest.raises(ValueError):
+        moe_shapes("W3", "EP", 1, 8, 8, 8, 4)
+
+
+@pytest.mark.parametrize("dtype", [None, torch.float32])
+def test_select_config_is_always_compiled(dtype):
+    pool = set(_MATMUL_CONFIG_POOL_F32 if dtype == torch.float32 else _MATMUL_CONFIG_POOL)
+    for m in (1, 8, 16, 17, 32, 64, 100, 512, 4096):
+        for n in (1, 31, 64, 65, 256, 4096):
+            for k in (1, 70, 128, 7168):
+                assert select_config(m, n, k, dtype) in pool
+
+
+def test_candidate_sets_are_bounded_unique_and_compiled():
+    for m in (1, 16, 32, 64, 128, 512):
+        for n in (3, 32, 64, 128, 512):
+            for k in (1, 32, 128, 8192):
+                single = matmul_candidate_configs(m, n, k)
+                assert 0 < len(single) <= 10 and len(set(single)) == len(single)
+                assert set(single) <= set(_MATMUL_CONFIG_POOL)
+                grouped = grouped_candidate_configs(m, n, k, problem_count=8, sm_count=16)
+                assert 0 < len(grouped) <= 36 and len(set(grouped)) == len(grouped)
+                for cfg in grouped:
+                    assert KernelConfig(**{**cfg.as_dict(), "cta_multiplier": 1}) in _GROUPED_BASE_CONFIG_POOL
+
+
+def test_grouped_candidates_cover_the_workload_families():
+    skinny = grouped_candidate_configs(8, 4096, 7168, problem_count=32, sm_count=256)
+    assert {c.block_m for c in skinny} <= {16, 32}
+    wide = grouped_candidate_configs(512, 4096, 7168, problem_count=32, sm_count=256)
+    assert any(c.block_m == 256 and c.block_n == 256 for c in wide)
+    assert {c.cta_multiplier for c in wide} >= {1, 2}
+    one = grouped_candidate_configs(16, 256, 7168, problem_count=1, sm_count=256)
+    assert {c.cta_multiplier for c in one} == {1}
+    tiny_grid = grouped_candidate_configs(16, 64, 64, problem_count=2, sm_count=256)
+    assert {c.cta_multiplier for c in tiny_grid} == {1}  # fewer tiles than CUs: no duplicate grids
+    fp32 = grouped_candidate_configs(64, 64, 64, problem_count=4, sm_count=256, dtype=torch.float32)
+    assert set(KernelConfig(**{**c.as_dict(), "cta_multiplier": 1}) for c in fp32) <= set(_MATMUL_CONFIG_POOL_F32)
+    with pytest.raises(ValueError):
+        grouped_candidate_configs(0, 1, 1)
+    with pytest.raises(ValueError):
+        grouped_candidate_configs(1, 1, 1, sm_count=-1)
+
+
+def test_diverse_configs_keeps_coverage_then_rank_order():
+    ranked = list(_MATMUL_CONFIG_POOL)
+    picked = diverse_configs(ranked, 5)
+    assert len(picked) == 5 and picked[0] == ranked[0]
+    assert len({(c.block_m, c.block_n) for c in picked}) >= 3
+    assert diverse_configs(ranked, 0) == ranked[:1]
+
+
+def test_shape_signature_is_order_sensitive_31_bit():
+    a = _shape_signature([(17, 13, 31), (1, 5, 3)])
+    b = _shape_signature([(1, 5, 3), (17, 13, 31)])
+    assert a != b and 0 <= a < 2**31 and a == _shape_signature([(17, 13, 31), (1, 5, 3)])
+
+
+def test_cpu_workspace_tables_and_flags():
+    shapes = [(1, 5, 3), (17, 13, 31), (9, 70, 65)]
+    ws = build_grouped_workspace(shapes, torch.bfloat16, seed=99, device="cpu")
+    assert ws.dims.tolist() == [[1, 3, 5], [17, 31, 13], [9, 65, 70]]
+    assert ws.strides.tolist()[2] == [70, 1, 65, 1, 65, 1]
+    assert ws.a_ptrs.tolist() == [t.data_ptr() for t in ws.a]
+    assert not ws.homogeneous and ws.problem_count == 3 and (ws.max_m, ws.max_n, ws.max_k) == (17, 65, 70)
+    assert ws.tile_count_for(KernelConfig(16, 64, 32, 1, 4, 2)) == 1 + 2 + 2
+    same = build_grouped_workspace([(17, 13, 31)] * 3, torch.float16, device="cpu")
+    assert same.homogeneous
+    strided = workspace_from_tensors([t.t() for t in same.b], [t.t() for t in same.a],
+                                     [torch.empty(31, 17, dtype=torch.float16) for _ in range(3)])
+    assert not strided.homogeneous
+    with pytest.raises(ValueError):
+        build_grouped_workspace([], torch.float16, device="cpu")
+    with pytest.raises(ValueError):
+        build_grouped_workspace([(1, 0, 3)], torch.float16, device="cpu")
+    with pytest.raises(ValueError):
+        build_fused_gate_up_workspace([(17, 13, 31)], torch.float16, device="cpu")
+    w13 = build_fused_gate_up_workspace([(17, 13, 62)] * 2, torch.float16, device="cpu")
+    assert w13.operation == "gate_up"
+
+
+def test_seeded_workspaces_are_reproducible():
+    first = build_grouped_workspace([(4, 8, 16)] * 2, torch.bfloat16, seed=7, device="cpu")
+    second = build_grouped_workspace([(4, 8, 16)] * 2, torch.bfloat16, seed=7, device="cpu")
+    assert all(torch.equal(x, y) for x, y in zip(first.a + first.b, second.a + second.b))
+
+
+def test_torch_grouped_workspace_layout_on_cpu():
+    ws = build_torch_grouped_workspace([(17, 13, 31)] * 3, torch.bfloat16, seed=104, device="cpu")
+    assert ws.offs.tolist() == [17, 34, 51]
+    assert ws.mat_a.stride(0) % 8 == 0 and ws.mat_b.stride(1) % 8 == 0
+    launch_torch_grouped(ws)
+    for a, b, c in ws.problem_tensors():
+        torch.testing.assert_close(c.float(), a.float() @ b.float(), rtol=2e-2, atol=2e-2)
+    with pytest.raises(ValueError):
+        build_torch_grouped_workspace([(17, 13, 31), (17, 14, 31)], torch.bfloat16, device="cpu")
+
+
+def test_grouped_trace_inspector_fails_closed():
+    compute = "void ck::kernel_grouped_gemm_xdl_splitk<...>"
+    ok = inspect_grouped_trace(["aten::_grouped_mm"], ["prepare_grouped_gemm_data", compute])
+    assert ok["grouped_compute_launches"] == 1 and ok["launches_per_iteration"] == 2
+    for cpu, gpu in (
+        (["aten::_grouped_mm", "aten::mm"], [compute]),
+        (["aten::_grouped_mm"], []),
+        (["aten::_grouped_mm"], ["Cijk_Ailk_Bljk_gemm", "Cijk_Ailk_Bljk_gemm"]),
+        (["aten::_grouped_mm"], [compute, "Memcpy DtoH"]),
+        (["aten::_grouped_mm"], [compute, compute]),
+        ([], [compute]),
+    ):
+        with pytest.raises(TorchGroupedMMUnavailable):
+            inspect_grouped_trace(cpu, gpu)
+
+
+def test_workspace_memory_estimates():
+    shapes = [(16, 64, 128)] * 2
+    assert _estimate(shapes, 2, "grouped") == 2 * 2 * (16 * 64 + 64 * 128 + 16 * 128) + 2 * 84
+    assert _estimate([(16, 13, 31)], 2, "torch") == 2 * (16 * 16 + 13 * 32 + 16 * 32) + 4
+
+
+def test_moe_experiment_has_no_single_mode(tmp_path):
+    args = SimpleNamespace(num_experts=8, parallel_size=4, ffn_size=16, hidden_size=32, topk=1, moe_ms=[1],
+                           tokens=None, torch_baseline=True, results_dir=tmp_path)
+    calls: list[str] = []
+
+    def fake_run_case(_args, _env, _projection, _parallel_type, mode, _m):
+        calls.append(mode)
+        return {"status": "skipped"}
+
+    with patch("benchmark_moe._run_case", side_effect=fake_run_case), patch("benchmark_moe.write_rows"):
+        run_moe(args, {})
+    assert set(calls) == {"grouped", "torch"}
+
+
+def test_moe_sweep_argument_checks(tmp_path):
+    base = dict(num_experts=8, parallel_size=4, ffn_size=16, hidden_size=32, topk=5, moe_ms=[3], tokens=None,
+                torch_baseline=False, results_dir=tmp_path)
+    with pytest.raises(ValueError, match="divisible by topk"):
+        run_moe(SimpleNamespace(**base), {})
+    with pytest.raises(ValueError, match="tokens"):
+        run_moe(SimpleNamespace(**{**base, "tokens": 3}), {})
+    with pytest.raises(ValueError):
+        run_moe(SimpleNamespace(**{**base, "parallel_size": 3}), {})
+
+
+def test_baseline_and_provenance_defaults():
+    assert parser().parse_args([]).torch_baseline
+    assert not parser().parse_args(["--no-torch-baseline"]).torch_baseline
+    for field in ("operation", "fused_projections", "output_layout", "activation_in_timed_region", "scheduler",
+                  "cta_multiplier", "output_preallocated", "best_measured_ratio", "near_best",
+                  "autotune_candidates_tested"):
+        assert field in CSV_FIELDS
+    assert len(CSV_FIELDS) == len(set(CSV_FIELDS)) == 87
+
+
+def test_csv_roundtrip(tmp_path):
+    path = tmp_path / "rows.csv"
+    write_rows(path, [{"M": 4, "status": "ok", "unknown_column": 1}])
+    rows = read_rows(path)
+    assert rows[0]["M"] == "4" and rows[0]["status"] == "ok" and "unknown_column" not in rows[0]
+    assert list(rows[0]) == CSV_FIELDS
+    assert read_rows(tmp_path / "absent.csv") == []
+
+
+def test_non_positive_cli_overrides_are_rejected():
+    for option in ("--hidden-size", "--ffn-size", "--num-experts", "--topk", "--heatmap-k"):
+        with pytest.raises(ValueError):
+            main([option, "0", "--no-plots"])
+    with pytest.raises(ValueError):
+        main(["--peak-tflops", "-1", "--no-plots"])
+    with pytest.raises(ValueError):
+        main(["--input-precision", "tf32", "--dtype", "bf16"])
+
+
+def test_derivable_metrics_are_recomputed():
+    row = {"M": "2", "K": "3", "N": "4", "num_gemms": "5", "total_flops": "240", "latency_ms": "2",
+           "tflops": "0.00000012"}
+    assert _derivable_metrics_valid(row)
+    assert not _derivable_metrics_valid({**row, "total_flops": "241"})
+    assert not _derivable_metrics_valid({**row, "tflops": "1"})
+    assert not _derivable_metrics_valid({**row, "latency_ms": "0"})
+
+
+GROUPED_ROW = {
+    "mode": "grouped", "autotune_enabled": "True", "autotune_status": "selected",
+    "config_source": "workload_autotune", "scheduler": "homogeneous_persistent", "launches_per_iteration": "1",
+    "output_preallocated": "True", "block_m": "256", "block_n": "256", "block_k": "64", "num_warps": "8",
+    "num_stages": "2", "cta_multiplier": "2",
+}
+
+
+def test_moe_execution_contract_requires_tuned_grouped_mode():
+    assert _moe_execution_contract_valid(GROUPED_ROW)
+    assert not _moe_execution_contract_valid({**GROUPED_ROW, "mode": "single"})
+    assert not _moe_execution_contract_valid({**GROUPED_ROW, "autotune_status": "not_run"})
+    assert not _moe_execution_contract_valid({**GROUPED_ROW, "launches_per_iteration": "2"})
+    assert not _moe_execution_contract_valid({**GROUPED_ROW, "num_stages": "0"})
+    torch_row = {"mode": "torch", "scheduler": "torch_grouped_mm", "launches_per_iteration": "2",
+                 "api_calls_per_iteration": "1", "grouped_compute_launches": "1", "execution_verified": "True",
+                 "output_preallocated": "False"}
+    assert _moe_execution_contract_valid(torch_row)
+    assert not _moe_execution_contract_valid({**torch_row, "execution_verified": "False"})
+    assert not _moe_execution_contract_valid({**torch_row, "scheduler": "sequential_torch_mm"})
+
+
+def test_projection_contract_records_gate_up_fusion():
+    gate_up = {"projection": "W1", "operation": "gate_up", "fused_projections": "2",
+               "output_layout": "gate_then_up", "activation_in_timed_region": "False"}
+    down = {"projection": "W2", "operation": "down", "fused_projections": "1", "output_layout": "down",
+            "activation_in_timed_region": "False"}
+    assert _projection_contract_valid(gate_up, "moe_w1.csv")
+    assert _projection_contract_valid(down, "moe_w2.csv")
+    assert not _projection_contract_valid({**gate_up, "fused_projections": "1"}, "moe_w1.csv")
+    assert not _projection_contract_valid({**down, "activation_in_timed_region": "True"}, "moe_w2.csv")
+
+
+def _moe_row(parallel_type: str, **extra):
+    m, k, n, g = 4, 8, 16, 2
+    flops = 2 * m * k * n * g
+    return {**GROUPED_ROW, "run_id": "r1", "status": "ok", "correct": "True", "projection": "W1",
+            "operation": "gate_up", "fused_projections": "2", "output_layout": "gate_then_up",
+            "activation_in_timed_region": "False", "M": str(m), "K": str(k), "N": str(n), "num_gemms": str(g),
+            "total_flops": str(flops), "latency_ms": "0.5", "tflops": repr(flops / (0.5 * 1e9)),
+            "flops_equal": "True", "parallel_type": parallel_type, "provider": "hip", "cache_mode": "hot",
+            "dtype": "bf16", "parallel_size": "4", "num_experts": "8", "topk": "2", "T": "16", **extra}
+
+
+def test_validate_results_end_to_end(tmp_path):
+    (tmp_path / "environment.json").write_text(json.dumps(
+        {"run_id": "r1", "requested_parameters": {"experiment": "moe", "no_plots": True}}))
+    write_rows(tmp_path / "moe_w1.csv", [_moe_row("EP"), _moe_row("TP")])
+    down = {"projection": "W2", "operation": "down", "fused_projections": "1", "output_layout": "down"}
+    write_rows(tmp_path / "moe_w2.csv", [_moe_row("EP", **down), _moe_row("TP", **down)])
+    report = validate_results(tmp_path, tmp_path / "plots")
+    assert report["valid"], report["issues"]
+    assert json.loads((tmp_path / "validation.json").read_text())["valid"]
+    write_rows(tmp_path / "moe_w2.csv", [_moe_row("EP", **down), _moe_row("TP", **down, total_flops="1")])
+    report = validate_results(tmp_path, tmp_path / "plots")
+    assert not report["valid"]
+    write_rows(tmp_path / "moe_w2.csv", [_moe_row("EP", **down, status="error")])
+    assert not validate_results(tmp_path, tmp_path / "plots")["valid"]

@@ -1,0 +1,165 @@
+"""GPU tests at the BASELINE configurations' full per-rank sizes, plus graph capture and timing.
+
+Full-size checks use properties that do not depend on size:
+  * exact-integer known answers on every expert (A = 1, B_e = e + 1 => C_e = K (e + 1), exact in
+    the fp32 accumulator and representable in bf16/fp16 for these K) - catches any wrong index,
+    missing tile, duplicated tile or tail error anywhere in the group;
+  * seeded random inputs checked on sampled experts against a float32 torch product on the GPU
+    (normwise max|C - R| / max|R| <= 1e-2 for bf16, <= 2e-3 for fp16) and on sampled rows against
+    the CPU oracle (same bound).
+"""
+
+from __future__ import annotations
+
+import time
+
+import pytest
+import torch
+
+from helpers import normwise, oracle_product
+
+pytestmark = pytest.mark.gpu
+
+NORMWISE = {torch.bfloat16: 1e-2, torch.float16: 2e-3}
+
+# (name, projection, parallel, M_e, H, F, E, P, dtype)
+CASES = [
+    ("dsv3_w1_ep_me8", "W1", "EP", 8, 7168, 2048, 256, 8, torch.bfloat16),
+    ("dsv3_w1_ep_me512", "W1", "EP", 512, 7168, 2048, 256, 8, torch.bfloat16),
+    ("dsv3_w1_tp_me64", "W1", "TP", 64, 7168, 2048, 256, 8, torch.bfloat16),
+    ("dsv3_w2_ep_me64", "W2", "EP", 64, 7168, 2048, 256, 8, torch.bfloat16),
+    ("dsv3_w2_tp_me512", "W2", "TP", 512, 7168, 2048, 256, 8, torch.bfloat16),
+    ("mixtral_w1_ep_me16", "W1", "EP", 16, 4096, 14336, 8, 8, torch.bfloat16),
+    ("mixtral_w2_ep_me128", "W2", "EP", 128, 4096, 14336, 8, 8, torch.bfloat16),
+    ("mixtral_w1_tp_me1024", "W1", "TP", 1024, 4096, 14336, 8, 8, torch.bfloat16),
+    ("mixtral_w2_tp_me16", "W2", "TP", 16, 4096, 14336, 8, 8, torch.bfloat16),
+    ("qwen3_w1_ep_me4", "W1", "EP", 4, 2048, 768, 128, 4, torch.float16),
+    ("qwen3_w1_tp_me256", "W1", "TP", 256, 2048, 768, 128, 4, torch.float16),
+    ("qwen3_w2_tp_me32", "W2", "TP", 32, 2048, 768, 128, 4, torch.float16),
+]
+
+
+@pytest.fixture(autouse=True)
+def _gpu_only():
+    if not torch.cuda.is_available():
+        pytest.skip("ROCm GPU unavailable")
+
+
+def _workspace(projection, parallel, m, h, f, e, p, dtype, seed=1234):
+    from kernels.grouped_gemm import build_fused_gate_up_workspace, build_grouped_workspace
+    from utils.metrics import moe_shapes
+
+    shapes = moe_shapes(projection, parallel, m, h, f, e, p)
+    builder = build_fused_gate_up_workspace if projection == "W1" else build_grouped_workspace
+    return builder(shapes, dtype, seed)
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_full_size_exact_integer_every_expert(case):
+    from kernels.grouped_gemm import launch_grouped
+
+    name, projection, parallel, m, h, f, e, p, dtype = case
+    print(f"exact full size {name}", flush=True)
+    workspace = _workspace(projection, parallel, m, h, f, e, p, dtype)
+    k = workspace.shapes[0][1]
+    for index, (a, b, c) in enumerate(workspace.problem_tensors()):
+        a.fill_(1)
+        b.fill_(index % 31 + 1)
+        c.fill_(float("nan"))
+    launch_grouped(workspace)  # autotuned: every candidate measured, the winner recorded
+    for c in workspace.c:
+        c.fill_(float("nan"))
+    launch_grouped(workspace, config=workspace.config, autotune=False)
+    torch.cuda.synchronize()
+    for index, c in enumerate(workspace.c):
+        expected = float(k * (index % 31 + 1))
+        assert torch.all(c == expected), f"{name}: expert {index} wrong with {workspace.config}"
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_full_size_random_sampled_against_references(case):
+    from kernels.grouped_gemm import launch_grouped
+
+    name, projection, parallel, m, h, f, e, p, dtype = case
+    print(f"random full size {name}", flush=True)
+    workspace = _workspace(projection, parallel, m, h, f, e, p, dtype)
+    launch_grouped(workspace)
+    for c in workspace.c:
+        c.fill_(float("nan"))
+    launch_grouped(workspace, config=workspace.config, autotune=False)
+    torch.cuda.synchronize()
+    experts = sorted({0, workspace.problem_count // 2, workspace.problem_count - 1})
+    for index in experts:
+        a, b, c = workspace.a[index], workspace.b[index], workspace.c[index]
+        assert torch.isfinite(c).all()
+        reference = a.float() @ b.float()
+        assert normwise(c, reference) <= NORMWISE[dtype], f"{name}: expert {index}"
+    a, b, c = workspace.a[-1], workspace.b[-1], workspace.c[-1]
+    rows = slice(max(0, a.shape[0] - 4), a.shape[0])  # tail rows of the last expert, full N
+    assert normwise(c[rows], oracle_product(a[rows], b)) <= NORMWISE[dtype]
+
+
+def test_heatmap_tail_shapes_against_oracle():
+    """Heatmap-style groups with non-multiple N/K (2880 = 22.5 x 128) and G in {1, 8}."""
+    from kernels.grouped_gemm import build_grouped_workspace, launch_grouped
+
+    for g, m, n, k in ((8, 32, 2880, 256), (1, 128, 1024, 2880), (8, 8, 256, 2880)):
+        print(f"heatmap sample G={g} M={m} N={n} K={k}", flush=True)
+        workspace = build_grouped_workspace([(m, k, n)] * g, torch.bfloat16, seed=g + m)
+        launch_grouped(workspace)
+        torch.cuda.synchronize()
+        for index in (0, g - 1):
+            a, b, c = workspace.a[index], workspace.b[index], workspace.c[index]
+            assert normwise(c, oracle_product(a, b)) <= 1e-2
+
+
+def test_graph_timing_excludes_host_delay_and_visits_cold_ring():
+    from utils.benchmark import time_cuda
+
+    outputs = [torch.zeros(16, device="cuda") for _ in range(4)]
+
+    def delayed(index):
+        time.sleep(0.02)
+        outputs[index].add_(1)
+
+    result = time_cuda(delayed, 2, 3, workspace_count=len(outputs))
+    assert result.repeat == 4
+    assert all(torch.equal(outputs[0], other) for other in outputs)
+    assert outputs[0][0].item() > 1
+    assert result.median_ms < 10
+
+
+def test_launch_grouped_is_graph_capturable_and_replays_match_eager():
+    from kernels.grouped_gemm import build_grouped_workspace, launch_grouped
+
+    workspace = build_grouped_workspace([(64, 512, 1024)] * 8, torch.bfloat16, seed=5)
+    launch_grouped(workspace)  # autotune outside capture
+    torch.cuda.synchronize()
+    eager = [c.clone() for c in workspace.c]
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        launch_grouped(workspace)  # cache hit: one kernel launch, captured
+    torch.cuda.synchronize()
+    for replay in range(3):
+        for c in workspace.c:
+            c.zero_()  # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for out, ref in zip(workspace.c, eager):
+            assert torch.equal(out, ref), f"replay {replay} differs from eager"
+
+
+def test_one_kernel_launch_per_call():
+    from kernels.grouped_gemm import build_grouped_workspace, launch_grouped
+
+    workspace = build_grouped_workspace([(32, 256, 512)] * 4, torch.bfloat16, seed=6)
+    launch_grouped(workspace)
+    torch.cuda.synchronize()
+    with torch.profiler.profile(activities=[torch.profiler.ProfilerActivity.CUDA]) as prof:
+        launch_grouped(workspace)
+        torch.cuda.synchronize()
+    names = [e.name for e in prof.events() if e.device_type == torch.autograd.DeviceType.CUDA]
+    assert sum("grouped_gemm_kernel" in n for n in names) == 1, names

@@ -1,0 +1,131 @@
+"""CPU tests of the C ABI boundary: the library loads, exports what include/moegemm.h declares,
+and rejects bad arguments with the documented codes before any GPU work."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from kernels import _native
+from kernels.matmul import _MENU_16BIT, _MENU_F32
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "moegemm.h"
+
+
+def _declarations() -> dict[str, int]:
+    """Function name -> parameter count, parsed from the header."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    found = {}
+    for match in re.finditer(r"\b(moegemm_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = match.group(2).strip()
+        found[match.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return found
+
+
+def test_header_declares_every_bound_symbol_and_nothing_else():
+    declared = _declarations()
+    assert set(declared) == set(_native.SIGNATURES)
+    for name, count in declared.items():
+        assert len(_native.SIGNATURES[name][1]) == count, name
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _native.library()
+    for name in _declarations():
+        assert hasattr(lib, name), name
+    assert lib.moegemm_abi_version() == _native.ABI_VERSION
+    header_version = int(re.search(r"#define MOEGEMM_ABI_VERSION (\d+)", HEADER.read_text()).group(1))
+    assert header_version == _native.ABI_VERSION
+
+
+def test_compiled_menus_match_python_candidate_pools():
+    assert [row[:5] for row in _native.compiled_kernels(_native.DTYPE_BF16)] == list(_MENU_16BIT)
+    assert [row[:5] for row in _native.compiled_kernels(_native.DTYPE_F16)] == list(_MENU_16BIT)
+    assert [row[:5] for row in _native.compiled_kernels(_native.DTYPE_F32)] == list(_MENU_F32)
+    for code in (_native.DTYPE_F16, _native.DTYPE_BF16, _native.DTYPE_F32):
+        for row in _native.compiled_kernels(code):
+            assert 0 < row[5] <= 160 * 1024  # LDS bytes fit one CU
+
+
+def _grouped(**overrides):
+    args = dict(a=1, b=1, c=1, dims=1, strides=1, g=4, m=16, n=64, k=64, homog=1, tiles=4, dtype=1, prec=0,
+                bm=256, bn=256, bk=64, group=8, warps=8, stages=2, grid=4, vec=1, stream=None)
+    args.update(overrides)
+    lib = _native.library()
+    return lib.moegemm_grouped_gemm(args["a"], args["b"], args["c"], args["dims"], args["strides"], args["g"],
+                                    args["m"], args["n"], args["k"], args["homog"], args["tiles"], args["dtype"],
+                                    args["prec"], args["bm"], args["bn"], args["bk"], args["group"], args["warps"],
+                                    args["stages"], args["grid"], args["vec"], args["stream"])
+
+
+@pytest.mark.parametrize("override, code, needle", [
+    ({"dtype": 7}, _native.ERR_INVALID, "dtype"),
+    ({"prec": 1}, _native.ERR_INVALID, "tf32"),
+    ({"prec": 5}, _native.ERR_INVALID, "precision"),
+    ({"group": 0}, _native.ERR_INVALID, "group_size_m"),
+    ({"bm": 48}, _native.ERR_NO_KERNEL, "no compiled kernel"),
+    ({"stages": 3}, _native.ERR_NO_KERNEL, "no compiled kernel"),
+    ({"g": 0}, _native.ERR_INVALID, "problem_count"),
+    ({"a": None}, _native.ERR_INVALID, "pointer tables"),
+    ({"m": 0}, _native.ERR_INVALID, "shape"),
+    ({"homog": 0, "dims": None}, _native.ERR_INVALID, "dims"),
+    ({"homog": 0, "tiles": -1}, _native.ERR_INVALID, "total_tiles"),
+])
+def test_grouped_entry_rejects_bad_arguments_without_launching(override, code, needle):
+    assert _grouped(**override) == code
+    assert needle in _native.last_error()
+
+
+def test_grouped_entry_with_no_tiles_is_a_no_op():
+    assert _grouped(homog=0, tiles=0) == _native.OK
+
+
+def test_matmul_entry_rejects_bad_arguments_without_launching():
+    lib = _native.library()
+    call = lambda **kw: lib.moegemm_matmul(
+        kw.get("a", 1), 1, 1, kw.get("m", 4), 4, 4, 4, 1, 4, 1, 4, 1, kw.get("dtype", 1), 0,
+        kw.get("bm", 16), 64, 128, 1, 4, 4, 0, None)
+    assert call(m=0) == _native.ERR_INVALID and "shape" in _native.last_error()
+    assert call(a=None) == _native.ERR_INVALID and "non-null" in _native.last_error()
+    assert call(bm=24) == _native.ERR_NO_KERNEL
+    assert call(dtype=3) == _native.ERR_INVALID
+
+
+def test_status_mapping_to_python_exceptions():
+    assert _grouped(dtype=9) == _native.ERR_INVALID
+    with pytest.raises(ValueError):
+        _native.check(_native.ERR_INVALID)
+    assert _grouped(bm=48) == _native.ERR_NO_KERNEL
+    with pytest.raises(RuntimeError):
+        _native.check(_native.ERR_NO_KERNEL)
+    _native.check(_native.OK)
+
+
+def test_launches_fail_loudly_without_a_gpu(monkeypatch):
+    import torch
+
+    from kernels.grouped_gemm import build_grouped_workspace, launch_grouped
+    from kernels.matmul import launch_matmul
+
+    workspace = build_grouped_workspace([(8, 16, 32)] * 2, torch.bfloat16, device="cpu")
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: False)
+    with pytest.raises(RuntimeError, match="GPU"):
+        launch_grouped(workspace)
+    with pytest.raises(ValueError):  # CPU tensors are rejected as a device mismatch first
+        launch_matmul(workspace.a[0], workspace.b[0], workspace.c[0])
+
+
+def test_missing_library_is_a_runtime_error(monkeypatch, tmp_path):
+    monkeypatch.setenv("MOEGEMM_LIBRARY", str(tmp_path / "absent.so"))
+    _native.library.cache_clear()
+    try:
+        with pytest.raises(RuntimeError, match="not built"):
+            _native.library()
+        assert not _native.available()
+    finally:
+        monkeypatch.delenv("MOEGEMM_LIBRARY")
+        _native.library.cache_clear()
+    assert isinstance(_native.library(), ctypes.CDLL)

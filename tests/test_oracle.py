@@ -1,0 +1,217 @@
+"""CPU tests that pin the oracle before it is trusted as the GPU checker.
+
+Each oracle function is checked against something it did not produce:
+  * golden vectors from torch CPU float64 (tests/golden/gemm_golden.npz, make_golden.py);
+  * closed forms (A = 1, B = e + 1 => C = k (e + 1), the reference's known-answer test,
+    tests/test_gpu.py:127-154) and a pure-Python brute force on tiny shapes;
+  * numpy float64 matmul for strided views, torch / numpy casts for the rounding functions;
+  * planted mistakes (a transposed operand, a dropped K term, a shifted column): each must fail the
+    same comparison that the oracle passes, so the comparison has teeth.
+"""
+
+from __future__ import annotations
+
+import itertools
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import oracle
+
+GOLDEN = np.load(Path(__file__).resolve().parent / "golden" / "gemm_golden.npz", allow_pickle=False)
+
+
+def _values(bits_or_f32: np.ndarray, dtype: str) -> np.ndarray:
+    return oracle.to_float(np.asarray(bits_or_f32), dtype).astype(np.float64)
+
+
+@pytest.mark.parametrize("name", [str(n) for n in GOLDEN["case_names"]])
+def test_gemm_matches_torch_float64_golden(name):
+    dtype = name.split("_")[0]
+    a, b = GOLDEN[f"{name}_a"], GOLDEN[f"{name}_b"]
+    out, sums = oracle.gemm(a, b, dtype, return_sums=True)
+    exact = GOLDEN[f"{name}_exact"]
+    if dtype == "fp32":
+        np.testing.assert_allclose(sums, exact, rtol=1e-12, atol=1e-15)
+        np.testing.assert_allclose(out, exact.astype(np.float32), rtol=2e-7, atol=1e-12)
+    else:
+        # Products of 16-bit values are exact and these sums fit a double: bit-exact both ways.
+        np.testing.assert_array_equal(sums, exact)
+        np.testing.assert_array_equal(out, GOLDEN[f"{name}_out"])
+
+
+def test_w13_packed_matches_golden_and_split_form():
+    a, b = GOLDEN["w13_fp16_a"], GOLDEN["w13_fp16_b"]
+    packed = oracle.gemm(a, b, "fp16")
+    np.testing.assert_array_equal(packed, GOLDEN["w13_fp16_out"])
+    np.testing.assert_array_equal(oracle.w13_reference(a, b, "fp16"), packed)
+
+
+def test_plumbing_case_sample_matches_golden():
+    a, bcols = GOLDEN["plumbing_a"], GOLDEN["plumbing_b_cols"]
+    rows = GOLDEN["plumbing_rows"]
+    out, sums = oracle.gemm(a, bcols, "bf16", return_sums=True)
+    picked = sums[rows, np.arange(len(rows))]
+    np.testing.assert_array_equal(picked, GOLDEN["plumbing_exact"])
+    np.testing.assert_array_equal(out[rows, np.arange(len(rows))], GOLDEN["plumbing_out"])
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
+@pytest.mark.parametrize("shape", [(1, 1, 1), (17, 33, 65), (3, 200, 7)])
+def test_known_answer_ones_times_index(dtype, shape):
+    m, k, n = shape
+    store = np.float32 if dtype == "fp32" else np.uint16
+    one = np.ones(1, np.float32)
+    encode = {"bf16": oracle.to_bf16_bits, "fp16": oracle.to_f16_bits, "fp32": lambda v: v.astype(np.float32)}[dtype]
+    a = np.full((m, k), encode(one)[0], dtype=store)
+    for e in range(3):
+        b = np.full((k, n), encode(np.array([e + 1.0], np.float32))[0], dtype=store)
+        out = oracle.gemm(a, b, dtype)
+        expected = np.full((m, n), k * (e + 1), dtype=np.float64)
+        np.testing.assert_array_equal(_values(out, dtype), _values(encode(expected.astype(np.float32)), dtype))
+
+
+def _brute(a_vals, b_vals):
+    m, k = len(a_vals), len(a_vals[0])
+    n = len(b_vals[0])
+    return [[math.fsum(a_vals[i][l] * b_vals[l][j] for l in range(k)) for j in range(n)] for i in range(m)]
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
+def test_brute_force_tiny(dtype):
+    rng = np.random.default_rng(5)
+    for m, k, n in [(1, 1, 1), (2, 3, 4), (5, 7, 3)]:
+        av = rng.standard_normal((m, k)).astype(np.float32)
+        bv = rng.standard_normal((k, n)).astype(np.float32)
+        if dtype == "fp32":
+            a, b = av, bv
+        else:
+            enc = oracle.to_bf16_bits if dtype == "bf16" else oracle.to_f16_bits
+            a, b = enc(av), enc(bv)
+        _, sums = oracle.gemm(a, b, dtype, return_sums=True)
+        expect = _brute(_values(a, dtype).tolist(), _values(b, dtype).tolist())
+        np.testing.assert_allclose(sums, np.array(expect), rtol=1e-13, atol=1e-13)
+
+
+def test_strided_views_match_numpy():
+    rng = np.random.default_rng(9)
+    base_a = rng.standard_normal((17, 140)).astype(np.float32)
+    base_b = rng.standard_normal((70, 130)).astype(np.float32)
+    a, b = base_a[:, ::2], base_b[:, ::2]  # non-unit inner strides
+    _, sums = oracle.gemm(a, b, "fp32", return_sums=True)
+    np.testing.assert_allclose(sums, a.astype(np.float64) @ b.astype(np.float64), rtol=1e-12, atol=1e-12)
+    bt = np.ascontiguousarray(base_b[:, :65].T).T  # column-major B
+    _, sums_t = oracle.gemm(a, bt, "fp32", return_sums=True)
+    np.testing.assert_allclose(sums_t, a.astype(np.float64) @ bt.astype(np.float64), rtol=1e-12, atol=1e-12)
+
+
+def test_fp32_accumulation_model_differs_only_by_rounding():
+    name = "bf16_40x256x320"
+    a, b = GOLDEN[f"{name}_a"], GOLDEN[f"{name}_b"]
+    _, s64 = oracle.gemm(a, b, "bf16", return_sums=True)
+    _, s32 = oracle.gemm(a, b, "bf16", accum="f32", return_sums=True)
+    scale = np.abs(s64).max()
+    assert 0 < np.abs(s32 - s64).max() / scale < 256 * 2.0**-24
+
+
+# ---------------------------------------------------------------------------------------------
+# Planted mistakes: the comparisons above must reject plausible implementation errors.
+
+def _mutant_transposed(a, b, dtype):
+    n = min(b.shape)
+    sq = np.ascontiguousarray(b[:n, :n].T)
+    return oracle.gemm(np.ascontiguousarray(a[:, :n]), sq, dtype)
+
+
+@pytest.mark.parametrize("mutant", ["transposed_b", "dropped_k_term", "shifted_column"])
+def test_planted_mistakes_fail_the_golden_comparison(mutant):
+    name = "fp16_33x70x65"
+    a, b = GOLDEN[f"{name}_a"], GOLDEN[f"{name}_b"]
+    good = GOLDEN[f"{name}_out"]
+    if mutant == "transposed_b":
+        got = _mutant_transposed(a, b, "fp16")
+        assert got.shape != good.shape or not np.array_equal(got, good)
+        sq_a, sq_b = a[:, :65], b[:65, :65]
+        np.testing.assert_raises(AssertionError, np.testing.assert_array_equal,
+                                 oracle.gemm(np.ascontiguousarray(sq_a), np.ascontiguousarray(sq_b.T), "fp16"),
+                                 oracle.gemm(np.ascontiguousarray(sq_a), np.ascontiguousarray(sq_b), "fp16"))
+    elif mutant == "dropped_k_term":
+        got = oracle.gemm(np.ascontiguousarray(a[:, :-1]), np.ascontiguousarray(b[:-1]), "fp16")
+        assert not np.array_equal(got, good)
+    else:
+        got = oracle.gemm(a, b, "fp16")
+        assert not np.array_equal(np.roll(got, 1, axis=1), good)
+
+
+# ---------------------------------------------------------------------------------------------
+# Rounding
+
+def test_bf16_rounding_matches_torch_casts():
+    values = GOLDEN["round_values"]
+    np.testing.assert_array_equal(oracle.to_bf16_bits(values), GOLDEN["round_bf16"])
+
+
+def test_fp16_rounding_matches_torch_and_numpy_casts():
+    values = GOLDEN["round_values"]
+    got = oracle.to_f16_bits(values)
+    np.testing.assert_array_equal(got, GOLDEN["round_fp16"])
+    with np.errstate(over="ignore"):  # values past the half range must become +-inf
+        np.testing.assert_array_equal(got, values.astype(np.float16).view(np.uint16))
+
+
+def test_bf16_nan_stays_nan_and_decoders_are_exact():
+    nan_bits = oracle.to_bf16_bits(np.array([np.nan], np.float32))
+    assert np.isnan(oracle.bf16_bits_to_float(nan_bits))[0]
+    all_f16 = np.arange(0, 65536, dtype=np.uint32).astype(np.uint16)
+    finite = (all_f16 & 0x7C00) != 0x7C00
+    np.testing.assert_array_equal(oracle.f16_bits_to_float(all_f16)[finite],
+                                  all_f16.view(np.float16).astype(np.float32)[finite])
+
+
+def test_tf32_rounding_ties_away_and_truncation_grid():
+    ulp = 2.0**-10
+    cases = {
+        1.0: 1.0,
+        1.0 + ulp / 2: 1.0 + ulp,          # tie -> away from zero
+        -(1.0 + ulp / 2): -(1.0 + ulp),
+        1.0 + ulp / 2 - 2.0**-23: 1.0,     # just below the tie -> down
+        1.0 + 3 * ulp / 2: 1.0 + 2 * ulp,  # tie -> away (not to even)
+    }
+    got = oracle.tf32_round(np.array(list(cases), np.float32))
+    np.testing.assert_array_equal(got, np.array(list(cases.values()), np.float32))
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal(1000).astype(np.float32)
+    assert np.all((oracle.tf32_round(x).view(np.uint32) & 0x1FFF) == 0)
+
+
+# ---------------------------------------------------------------------------------------------
+# Tables and launch rules (kernels/grouped_gemm.py:530-552, 597-640)
+
+def test_tables_order_and_dispatch_rules():
+    shapes = [(1, 5, 3), (17, 13, 31), (9, 70, 65)]
+    dims, strides = oracle.tables(shapes)
+    assert dims.tolist() == [[1, 3, 5], [17, 31, 13], [9, 65, 70]]
+    assert strides.tolist()[1] == [13, 1, 31, 1, 31, 1]
+    assert oracle.dispatch(1, True) == "single_problem_matmul"
+    assert oracle.dispatch(3, True) == "homogeneous_persistent"
+    assert oracle.dispatch(3, False) == "generic_persistent"
+    assert oracle.is_homogeneous([(17, 13, 31)] * 3, [True] * 9)
+    assert not oracle.is_homogeneous(shapes, [True] * 9)
+    assert not oracle.is_homogeneous([(17, 13, 31)] * 3, [True] * 8 + [False])
+    # (1,5,3): 1x1 tiles; (17,13,31): 2x1; (9,70,65): 1x2.
+    assert oracle.grid_size(shapes, 16, 64, 120, 2) == 1 + 2 + 2
+    assert oracle.grid_size([(4096, 8, 4096)] * 4, 128, 128, 120, 2) == 240
+
+
+@pytest.mark.parametrize("group_m", [1, 4, 8])
+@pytest.mark.parametrize("grid", [1, 7, 64])
+def test_tile_order_visits_every_tile_once(group_m, grid):
+    shapes = [(1, 5, 3), (130, 40, 300), (64, 8, 64), (257, 9, 129)]
+    visits = oracle.tile_order(shapes, 64, 64, group_m, grid)
+    flat = list(itertools.chain.from_iterable(visits))
+    expected = {(e, tm, tn) for e, (m, _, n) in enumerate(shapes)
+                for tm in range(math.ceil(m / 64)) for tn in range(math.ceil(n / 64))}
+    assert len(flat) == len(expected) == oracle.tile_count(shapes, 64, 64)
+    assert set(flat) == expected
