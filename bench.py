@@ -148,7 +148,7 @@ def _cpu_baseline(seconds_target: float = 12.0) -> dict:
     cols = 256
     oracle.gemm_fast_bf16(a[:16], b[:, :cols], threads)  # warm (thread pool, pages)
     done_flops, elapsed, slices = 0, 0.0, 0
-    while elapsed < seconds_target and slices < 64:
+    while elapsed < seconds_target and slices < 4096:
         t0 = time.perf_counter()
         oracle.gemm_fast_bf16(a, np.ascontiguousarray(b[:, (slices * cols) % n:(slices * cols) % n + cols]), threads)
         elapsed += time.perf_counter() - t0
@@ -171,6 +171,8 @@ def main(argv=None) -> int:
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--no-cases", action="store_true", help="only the headline case")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    parser.add_argument("--copy-calibration", type=int, metavar="MIB", default=0,
+                        help="only run a plain device copy of MIB MiB (HBM counter calibration) and exit")
     args = parser.parse_args(argv)
     if args.gpus != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (every GPU box here has "
@@ -183,6 +185,14 @@ def main(argv=None) -> int:
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a ROCm GPU")
     torch.cuda.set_device(0)
+    if args.copy_calibration:
+        src = torch.empty(args.copy_calibration << 20, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": src.numel(), "launches": args.steps}))
+        return 0
     headline = _case("W1", "EP", 512, args.steps, args.warmup)
     cases = []
     if not args.no_cases:

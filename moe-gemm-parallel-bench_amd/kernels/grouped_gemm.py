@@ -99,13 +99,16 @@ def grouped_candidate_configs(
     sm_count: int = 0,
     dtype=None,
 ) -> tuple[KernelConfig, ...]:
-    """Workload-aware tile and persistent-grid candidates (at most 3 * base_limit).
+    """Workload-aware tile and persistent-grid candidates (at most 36).
 
-    Tiles are ranked by ``estimate_seconds`` on the whole group, so a narrow N tile that exposes
-    enough expert tiles to fill the device can outrank a better-padded wide one.  Each kept tile
-    gets cta_multiplier 1 plus 2 (and 4 for skinny tiles) only when the group has more tiles than
-    one grid's worth, so no two candidates launch the same grid.  A single problem dispatches to
-    the single-GEMM path, whose candidates carry cta_multiplier 1 only.
+    Tile shapes (block_m, block_n) are ranked by ``estimate_seconds`` on the whole group, so a narrow
+    N tile that exposes enough expert tiles to fill the device can outrank a better-padded wide one.
+    The best-ranked shapes keep every compiled variant (block_k, waves, LDS stages), because the
+    cost model cannot tell those apart and measurement can; GROUP_M variants are added only when a
+    problem spans several M tiles (otherwise traversal order is the same).  Each kept config gets
+    cta_multiplier 1, plus 2 (and 4 for skinny tiles) only when the group has more tiles than one
+    grid's worth, so no two candidates launch the same grid.  A single problem dispatches to the
+    single-GEMM path, whose candidates carry cta_multiplier 1 only.
     """
     if min(max_m, max_n, max_k, problem_count) <= 0:
         raise ValueError("grouped candidate dimensions and problem_count must be positive")
@@ -120,31 +123,36 @@ def grouped_candidate_configs(
     f32 = _is_f32(dtype)
     element_size = 4 if f32 else 2
     shapes = [(max_m, max_k, max_n)] * problem_count
-    pool = config_pool(dtype)
-    m_cap = max(16, 2 ** math.ceil(math.log2(max_m)))
-    family = [cfg for cfg in pool if cfg.block_m <= m_cap] or list(pool)
-    fallback = select_config(max_m, max_n, max_k, dtype)
-    if fallback not in family:
-        family.append(fallback)
     units = sm_count or 256
-    ranked = sorted(
-        family,
-        key=lambda cfg: (estimate_seconds(shapes, cfg, element_size, units, f32),
-                         -cfg.block_m * cfg.block_n, cfg.block_k, cfg.group_size_m),
-    )
+    m_cap = max(16, 2 ** math.ceil(math.log2(max_m)))
+    pool = [cfg for cfg in config_pool(dtype) if cfg.block_m <= m_cap] or list(config_pool(dtype))
+    by_tile: dict[tuple[int, int], list[KernelConfig]] = {}
+    for cfg in pool:
+        by_tile.setdefault((cfg.block_m, cfg.block_n), []).append(cfg)
+    score = {tile: min(estimate_seconds(shapes, cfg, element_size, units, f32) for cfg in cfgs)
+             for tile, cfgs in by_tile.items()}
+    tiles = sorted(by_tile, key=lambda t: (score[t], -t[0] * t[1]))
     candidates: list[KernelConfig] = []
-    for cfg in diverse_configs(ranked, base_limit):
-        tiles = problem_count * math.ceil(max_m / cfg.block_m) * math.ceil(max_n / cfg.block_n)
+    limit = 36
+    for tile in tiles:
+        several_m_tiles = math.ceil(max_m / tile[0]) > 1
+        variants = [cfg for cfg in by_tile[tile] if cfg.group_size_m in ((1, 8) if several_m_tiles else (8,))]
+        tile_count = problem_count * math.ceil(max_m / tile[0]) * math.ceil(max_n / tile[1])
         multipliers = [1]
-        if not sm_count or tiles > sm_count:
+        if not sm_count or tile_count > sm_count:
             multipliers.append(2)
-        if cfg.block_m <= 32 and (not sm_count or tiles > 2 * sm_count):
+        if tile[0] <= 32 and (not sm_count or tile_count > 2 * sm_count):
             multipliers.append(4)
-        candidates.extend(
-            KernelConfig(cfg.block_m, cfg.block_n, cfg.block_k, cfg.group_size_m, cfg.num_warps,
-                         cfg.num_stages, mult)
-            for mult in multipliers
-        )
+        expanded = [KernelConfig(c.block_m, c.block_n, c.block_k, c.group_size_m, c.num_warps, c.num_stages, mult)
+                    for c in variants for mult in multipliers]
+        if candidates and len(candidates) + len(expanded) > limit:
+            break
+        candidates.extend(expanded[: limit - len(candidates)])
+        if len({(c.block_m, c.block_n) for c in candidates}) >= max(1, base_limit // 3):
+            break
+    fallback = select_config(max_m, max_n, max_k, dtype)
+    if not any(c.tile_key == fallback.tile_key for c in candidates) and len(candidates) < limit:
+        candidates.append(fallback)
     return tuple(dict.fromkeys(candidates))
 
 
