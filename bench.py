@@ -65,14 +65,17 @@ def _check_sample(workspace, experts=(0, -1)) -> float:
     return worst
 
 
-def _time_steps(workspace, steps: int, warmup: int) -> tuple[float, float]:
+def _time_steps(workspace, steps: int, warmup: int, pinned) -> tuple[float, float]:
     """(ms per step from HIP events on the launch stream, wall ms per step)."""
     import torch
 
     from kernels.grouped_gemm import launch_grouped
 
+    def step():
+        launch_grouped(workspace, config=pinned, autotune=pinned is None)
+
     for _ in range(warmup):
-        launch_grouped(workspace, autotune=True)
+        step()
     stream = torch.cuda.current_stream()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
@@ -80,27 +83,29 @@ def _time_steps(workspace, steps: int, warmup: int) -> tuple[float, float]:
     wall = time.perf_counter()
     start.record(stream)
     for _ in range(steps):
-        launch_grouped(workspace, autotune=True)
+        step()
     end.record(stream)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - wall) * 1e3
     return start.elapsed_time(end) / steps, wall / steps
 
 
-def _case(projection: str, parallel_type: str, m: int, steps: int, warmup: int, seed: int = 1234) -> dict:
+def _case(projection: str, parallel_type: str, m: int, steps: int, warmup: int, seed: int = 1234,
+          pinned=None) -> dict:
+    """Time one DSV3 case; ``pinned`` (a KernelConfig) skips autotuning."""
     import torch
 
     from kernels.grouped_gemm import launch_grouped
     from utils.metrics import gemm_bytes, gemm_flops
 
     workspace = _workspace(projection, parallel_type, m, seed)
-    launch_grouped(workspace, autotune=True)  # autotune (untimed) on a cache miss
+    launch_grouped(workspace, config=pinned, autotune=pinned is None)  # autotune (untimed) on a cache miss
     for c in workspace.c:
         c.fill_(float("nan"))
-    launch_grouped(workspace, autotune=True)
+    launch_grouped(workspace, config=pinned, autotune=pinned is None)
     torch.cuda.synchronize()
     error = _check_sample(workspace)
-    ms, wall_ms = _time_steps(workspace, steps, warmup)
+    ms, wall_ms = _time_steps(workspace, steps, warmup, pinned)
     flops = sum(gemm_flops(*s) for s in workspace.shapes)
     nbytes = sum(gemm_bytes(*s, 2) for s in workspace.shapes)
     tflops = flops / (ms * 1e9)
@@ -171,6 +176,8 @@ def main(argv=None) -> int:
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--no-cases", action="store_true", help="only the headline case")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    parser.add_argument("--kernel-config", metavar="BM,BN,BK,WARPS,STAGES,GROUP_M,MULT", default=None,
+                        help="pin the headline kernel config instead of autotuning (counter passes)")
     parser.add_argument("--copy-calibration", type=int, metavar="MIB", default=0,
                         help="only run a plain device copy of MIB MiB (HBM counter calibration) and exit")
     args = parser.parse_args(argv)
@@ -193,7 +200,13 @@ def main(argv=None) -> int:
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes": src.numel(), "launches": args.steps}))
         return 0
-    headline = _case("W1", "EP", 512, args.steps, args.warmup)
+    pinned = None
+    if args.kernel_config:
+        from kernels.matmul import KernelConfig
+
+        bm, bn, bk, warps, stages, group, mult = (int(v) for v in args.kernel_config.split(","))
+        pinned = KernelConfig(bm, bn, bk, group, warps, stages, mult)
+    headline = _case("W1", "EP", 512, args.steps, args.warmup, pinned=pinned)
     cases = []
     if not args.no_cases:
         for projection, parallel_type, m in (("W1", "EP", 8), ("W1", "TP", 512), ("W1", "TP", 8),
