@@ -10,11 +10,14 @@
 //    wave instruction moves 1 KiB: lane l's 16 bytes land at M0 + 16*l, so each lane fetches the
 //    global chunk that the XOR swizzle assigns to its LDS slot.
 //  * STAGES LDS buffers form a ring; STAGES-1 slices are in flight while the MFMAs consume the
-//    current one.  The compiler does not track LDS-DMA completion, so the loop waits explicitly:
-//    s_waitcnt vmcnt(<loads issued after the current slice>) then s_barrier (each wave has seen
-//    its own copies land; the barrier makes that true for all waves).  The slice refilled after
-//    the barrier is the one every wave finished reading in the previous iteration, so one
-//    barrier per K slice suffices.  Compiler memory barriers keep LDS reads from moving across.
+//    current one.  The copies are issued from inline asm, so the compiler neither sees nor waits
+//    on them (its own tracking would put s_waitcnt vmcnt(0) before every ds_read_b64_tr_b16,
+//    serialising each K slice behind the newest copies' global-memory latency).  The loop waits
+//    explicitly instead: s_waitcnt vmcnt(<copies issued after the slice it needs>) then s_barrier
+//    (each wave has seen its own copies land; the barrier makes that true for all waves).  The
+//    slice refilled after the barrier is the one every wave finished reading in the previous
+//    iteration, so one barrier per K slice suffices.  Compiler memory barriers keep LDS reads
+//    from moving across.  No other vector-memory loads are issued while copies are in flight.
 //  * Fragment reads for K step kk+1 are issued before the MFMAs of step kk (register double
 //    buffering) so the MFMA pipe does not wait on LDS latency inside a slice.
 // Preconditions (checked by the host before choosing this variant): fp16/bf16, unit inner strides,
@@ -29,9 +32,32 @@ namespace moegemm {
 constexpr uint32_t kBufferFlags = 0x00020000u;
 constexpr uint32_t kOutOfRange = 0x80000000u;
 
-#define MOEGEMM_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
-
 __device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
+
+// Raw buffer resource (V#) for untyped loads: 48-bit base, stride 0, num_records bytes.
+__device__ __forceinline__ u32x4_t make_rsrc(const void* base, uint32_t num_records) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return u32x4_t{(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, num_records, kBufferFlags};
+}
+
+// LDS byte address of a shared-memory pointer (what M0 holds for an LDS-DMA copy).
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)(p));
+}
+
+// One LDS-DMA copy: every lane reads 16 bytes at rsrc.base + voffset (zero when voffset is past
+// num_records) and the wave's 64 x 16 bytes land contiguously at LDS byte address `lds`.  M0
+// holds the LDS address; one wait state separates the M0 write from the copy that reads it.
+// M0 has no other use in these kernels (gfx9 LDS instructions do not read it).
+__device__ __forceinline__ void dma_copy16(u32x4_t rsrc, uint32_t voffset, uint32_t lds) {
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voffset), "s"(rsrc), "s"(lds)
+               : "memory", "m0");
+#pragma clang diagnostic pop
+}
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -80,24 +106,24 @@ struct FastTile {
   using acc_t = typename std::conditional<ACC == 16, f32x16_t, f32x4_t>::type;
 
   struct Dma {
-    __amdgpu_buffer_rsrc_t ra, rb;
+    u32x4_t ra, rb;
     uint32_t a_off[QA];  // byte offset at k0 = 0, or kOutOfRange
     uint32_t a_kch[QA];  // k index of the lane's chunk at k0 = 0
     uint32_t b_off[QB];
     int32_t k;
     uint32_t ldb_bytes;
+    uint32_t lds_wave;   // LDS byte address of this wave's first 1 KiB slot in stage 0
   };
 
-  __device__ static __forceinline__ void setup_dma(Dma& d, const ProblemDesc& pd, int m0, int n0) {
+  __device__ static __forceinline__ void setup_dma(Dma& d, const ProblemDesc& pd, int m0, int n0, const char* smem) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t lda_bytes = (uint32_t)pd.sam * 2u;
     d.ldb_bytes = (uint32_t)pd.sbk * 2u;
     d.k = pd.k;
     const int rows = min(BM, pd.m - m0);
-    d.ra = __builtin_amdgcn_make_buffer_rsrc((void*)(pd.a + (int64_t)m0 * lda_bytes), 0,
-                                             (int)((uint32_t)rows * lda_bytes), kBufferFlags);
-    d.rb = __builtin_amdgcn_make_buffer_rsrc((void*)(pd.b + (int64_t)n0 * 2), 0,
-                                             (int)((uint32_t)pd.k * d.ldb_bytes - (uint32_t)n0 * 2u), kBufferFlags);
+    d.ra = make_rsrc(pd.a + (int64_t)m0 * lda_bytes, (uint32_t)rows * lda_bytes);
+    d.rb = make_rsrc(pd.b + (int64_t)n0 * 2, (uint32_t)pd.k * d.ldb_bytes - (uint32_t)n0 * 2u);
+    d.lds_wave = lds_address(smem) + (uint32_t)__builtin_amdgcn_readfirstlane(wave) * 1024u;
 #pragma unroll
     for (int q = 0; q < QA; ++q) {
       const int j = wave + q * NW;
@@ -118,15 +144,16 @@ struct FastTile {
   }
 
   // Copy K slice [k0, k0 + BK) into LDS stage `stage`.
-  __device__ static __forceinline__ void issue_stage(const Dma& d, char* smem, int stage, int k0) {
-    const int wave = threadIdx.x >> 6;
-    char* base = smem + stage * STAGE_BYTES;
+  // Slot j of a stage is written by wave j % NW; `wave` below is wave-uniform.
+  __device__ static __forceinline__ void issue_stage(const Dma& d, int stage, int k0) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t base = d.lds_wave + (uint32_t)(stage * STAGE_BYTES);
 #pragma unroll
     for (int q = 0; q < QA; ++q) {
       const int j = wave + q * NW;
       if (IA % NW == 0 || j < IA) {
         const uint32_t off = ((int)d.a_kch[q] + k0 < d.k) ? d.a_off[q] + (uint32_t)k0 * 2u : kOutOfRange;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(d.ra, MOEGEMM_LDS_PTR(base + j * 1024), 16, off, 0, 0, 0);
+        dma_copy16(d.ra, off, base + (uint32_t)(q * NW * 1024));
       }
     }
     const uint32_t kstep = (uint32_t)k0 * d.ldb_bytes;
@@ -135,8 +162,7 @@ struct FastTile {
       const int j = wave + q * NW;
       if (IB % NW == 0 || j < IB) {
         const uint32_t off = d.b_off[q] == kOutOfRange ? kOutOfRange : d.b_off[q] + kstep;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(d.rb, MOEGEMM_LDS_PTR(base + A_BYTES + j * 1024), 16, off, 0, 0,
-                                                 0);
+        dma_copy16(d.rb, off, base + (uint32_t)(A_BYTES + q * NW * 1024));
       }
     }
   }
@@ -266,7 +292,7 @@ struct FastTile {
     const int wave_m = wave / WN, wave_n = wave % WN;
     const int m0 = tm * BM, n0 = tn * BN;
     Dma d;
-    setup_dma(d, pd, m0, n0);
+    setup_dma(d, pd, m0, n0, smem);
 
     acc_t acc[FM][FN];
 #pragma unroll
@@ -279,7 +305,7 @@ struct FastTile {
     // Prologue: slices 0..STAGES-1 in flight, then slice 0 resident and its first fragments read.
     // Slices at or past K read out of range and land as zeros, so every copy is unconditional.
 #pragma unroll
-    for (int s = 0; s < STAGES; ++s) issue_stage(d, smem, s, s * BK);
+    for (int s = 0; s < STAGES; ++s) issue_stage(d, s, s * BK);
     wait_vmcnt<(STAGES - 1) * XMIN>();
     compiler_fence();
     __builtin_amdgcn_s_barrier();
@@ -307,7 +333,7 @@ struct FastTile {
       compiler_fence();
       __builtin_amdgcn_s_barrier();
       compiler_fence();
-      issue_stage(d, smem, kt % STAGES, (kt + STAGES) * BK);
+      issue_stage(d, kt % STAGES, (kt + STAGES) * BK);
       load_frags(af[0], bf[0], nxt, nxt + A_BYTES, 0, wave_m, wave_n);
       mfma_rows<HALF, FM>(acc, af[L], bf[L]);
       interleave<(FM - HALF) * FN, NDS, NVM>();

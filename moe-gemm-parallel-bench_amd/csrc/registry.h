@@ -53,6 +53,7 @@ hipError_t launch_tile(const KParams& p, int grid, hipStream_t stream) {
 // STAGES is sized to the 160 KiB LDS of a CU.
 #define MOEGEMM_MENU_16BIT(X, E)                                                             \
   X(E, 256, 256, 64, 2, 4, 2) X(E, 256, 256, 64, 2, 2, 2) X(E, 256, 256, 32, 2, 2, 4)        \
+  X(E, 256, 256, 32, 2, 4, 4)                                                                \
   X(E, 256, 128, 64, 2, 2, 3) X(E, 128, 256, 64, 2, 4, 3)                                   \
   X(E, 128, 256, 64, 2, 2, 3) X(E, 128, 128, 64, 2, 2, 4) X(E, 128, 64, 64, 2, 2, 4)         \
   X(E, 64, 256, 64, 1, 4, 3) X(E, 64, 128, 64, 2, 2, 4) X(E, 64, 64, 64, 2, 2, 4)            \

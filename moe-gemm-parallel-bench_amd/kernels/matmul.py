@@ -47,7 +47,7 @@ class KernelConfig:
 # Compiled tile menus: (block_m, block_n, block_k, num_warps, num_stages).  They must equal the
 # X-macro menus of csrc/registry.h; tests/test_native_abi.py compares them with the library.
 _MENU_16BIT: tuple[tuple[int, int, int, int, int], ...] = (
-    (256, 256, 64, 8, 2), (256, 256, 64, 4, 2), (256, 256, 32, 4, 4),
+    (256, 256, 64, 8, 2), (256, 256, 64, 4, 2), (256, 256, 32, 4, 4), (256, 256, 32, 8, 4),
     (256, 128, 64, 4, 3), (128, 256, 64, 8, 3), (128, 256, 64, 4, 3), (128, 128, 64, 4, 4), (128, 64, 64, 4, 4),
     (64, 256, 64, 4, 3), (64, 128, 64, 4, 4), (64, 64, 64, 4, 4),
     (32, 256, 64, 4, 4), (32, 128, 64, 4, 4), (32, 128, 128, 4, 3),
