@@ -157,12 +157,18 @@ __device__ __forceinline__ void store1<EF32>(char* dst, float v) { *reinterpret_
 
 // ---------------------------------------------------------------------------------------------
 // XOR swizzles on 16-byte chunk indices (see header comment).
+// Both were chosen with the SQ_LDS_BANK_CONFLICT counter on gfx950 over every fragment-read
+// pattern the tiles use (ds_read_b128 A reads with the 32x32 and 16x16 MFMA lane maps at 4, 8 and
+// 16 chunks per row; ds_read_b64_tr_b16 B reads at 8, 16 and 32 chunks per row): each read then
+// takes the minimum LDS cycles (4 for b128, 2 for tr_b64).
 __device__ __forceinline__ int swz_a(int row, int chunks) {
-  int f = (chunks >= 16) ? (row & 15) : (chunks == 8) ? ((row & 7) ^ ((row >> 3) & 1))
-                                     : ((row >> 1) ^ (row >> 3));
+  int f = (chunks >= 16) ? (row & 15) : (row ^ (row >> 2));
   return f & (chunks - 1);
 }
 __device__ __forceinline__ int swz_b(int row, int chunks) {
+  // Independent of row bit 2: the transpose reads fetch rows r and r + 4 (r bit 2 clear) with
+  // one chunk index.
+  if (chunks == 8) return ((row << 1) & 4) | ((row >> 2) & 2);
   // h = [0, 3, 6, 5] on row bits 0-1, doubled to chunk pairs, plus row bit 3 moving by 8 chunks.
   int r = row & 3;
   int h = (r << 1) ^ r;

@@ -6,6 +6,7 @@
 
 #include "gemm_fast.h"
 #include "gemm_kernel.h"
+#include "gemm_pingpong.h"
 
 namespace moegemm {
 
@@ -30,7 +31,16 @@ hipError_t launch_tile(const KParams& p, int grid, hipStream_t stream) {
 
 // X-macro menus: X(E, BM, BN, BK, WAVES_M, WAVES_N, STAGES).  Each translation unit expands a
 // menu into explicit kernel instantiations (device and host passes) and into the host table.
-#define MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S) FastTile<E, BM, BN, BK, WM, WN, S>
+// The 8-wave 256x256 tiles with at least three stages run the ping-pong schedule
+// (gemm_pingpong.h); every other 16-bit vector-layout tile runs FastTile's schedule.
+template <class E, int BM, int BN, int BK, int WM, int WN, int S>
+struct FastTileFor {
+  using type = typename std::conditional<BM == 256 && BN == 256 && WM == 2 && WN == 4 && S >= 3,
+                                         PingPongTile<E, BK, S>, FastTile<E, BM, BN, BK, WM, WN, S>>::type;
+};
+template <class E, int BM, int BN, int BK, int WM, int WN, int S>
+using FastTileT = typename FastTileFor<E, BM, BN, BK, WM, WN, S>::type;
+#define MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S) FastTileT<E, BM, BN, BK, WM, WN, S>
 #define MOEGEMM_GEN(E, BM, BN, BK, WM, WN) GemmTile<E, BM, BN, BK, WM, WN>
 
 #define MOEGEMM_INST16(E, BM, BN, BK, WM, WN, S)                                              \
