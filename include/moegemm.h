@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define MOEGEMM_ABI_VERSION 2
+#define MOEGEMM_ABI_VERSION 3
 
 #define MOEGEMM_OK 0
 #define MOEGEMM_ERR_INVALID (-1)   /* bad shape, pointer, dtype or parameter (Python: ValueError) */
@@ -75,6 +75,29 @@ int moegemm_grouped_gemm(const int64_t* a_ptrs, const int64_t* b_ptrs, const int
                          int32_t dtype, int32_t input_precision, int32_t block_m, int32_t block_n,
                          int32_t block_k, int32_t group_size_m, int32_t num_warps,
                          int32_t num_stages, int32_t grid_size, int32_t vector_layout, void* stream);
+
+/*
+ * Grouped GEMM over the expert-sorted layout of torch.nn.functional.grouped_mm (2-D A, 3-D B):
+ * for each group e, C[r0:r1, :] = A[r0:r1, :] @ B[e] with r0 = offs[e-1] (0 for e = 0) and
+ * r1 = offs[e], fp32 accumulation.  A is [rows, k] (row stride stride_am), B is [group_count, k, n]
+ * (strides stride_bg, stride_bk), C is [rows, n] (row stride stride_cm), all with unit inner stride;
+ * offs is a device int32 [group_count] array of cumulative end rows that the kernel reads at run
+ * time (it may be produced on the device by a router; no host copy is needed).  Offsets are
+ * clamped to [0, rows] and a decreasing offset is an empty group, so no access leaves A or C; rows
+ * at or past offs[group_count-1] are not written.  Replaces the one-call grouped_mm provider of
+ * reference kernels/torch_grouped_gemm.py:121-174 (build_torch_grouped_workspace +
+ * launch_torch_grouped; layout :139-158) with the persistent HIP kernel: the grid walks an upper
+ * bound of the tile count computed on the host from rows and group_count and stops at the total
+ * computed on the device from offs.  Tile config and grid_size as for moegemm_grouped_gemm; the
+ * LDS-DMA kernel is chosen automatically when the layout allows it.
+ */
+int moegemm_grouped_mm_offs(const void* a, const void* b, void* c, const int32_t* offs,
+                            int32_t group_count, int32_t rows, int32_t n, int32_t k,
+                            int64_t stride_am, int64_t stride_bg, int64_t stride_bk,
+                            int64_t stride_cm, int32_t dtype, int32_t input_precision,
+                            int32_t block_m, int32_t block_n, int32_t block_k,
+                            int32_t group_size_m, int32_t num_warps, int32_t num_stages,
+                            int32_t grid_size, void* stream);
 
 /*
  * Masked single GEMM with arbitrary strides, C = A @ B.  Replaces the Triton launch of

@@ -71,6 +71,8 @@ def parser() -> argparse.ArgumentParser:
     p.add_argument("--seed", type=int, default=1234)
     p.add_argument("--torch-baseline", action=argparse.BooleanOptionalAction, default=True,
                    help="Add torch.mm single-GEMM baselines and a torch grouped_mm MoE baseline")
+    p.add_argument("--offsets-layout", action=argparse.BooleanOptionalAction, default=False,
+                   help="Add MoE rows of the HIP kernel over the expert-sorted 2-D A / 3-D B / offsets layout")
     p.add_argument("--shape-k", type=int, default=4096)
     p.add_argument("--shape-product", type=int, default=1024 * 1024)
     p.add_argument("--shape-ms", type=int_list)

@@ -1,8 +1,10 @@
 """Per-rank EP versus TP MoE expert GEMMs at equal useful FLOPs (uniform top-k routing, no router).
 
 Same experiment as the reference's benchmark_moe.py: for W1 (packed Gate+Up) and W2 (Down), each
-tokens-per-expert M_e, each mode (``grouped`` = this project's HIP kernel, ``torch`` = one verified
-``torch.nn.functional.grouped_mm`` call) and each parallel type, the case
+tokens-per-expert M_e, each mode (``grouped`` = this project's HIP kernel over per-expert pointer
+tables, ``offsets`` = the same kernel over the expert-sorted 2-D A / 3-D B / int32 offsets layout
+(opt-in, ``--offsets-layout``), ``torch`` = one verified ``torch.nn.functional.grouped_mm`` call)
+and each parallel type, the case
   1. checks exact EP/TP FLOP equality and builds the per-rank shapes (utils/metrics.py);
   2. admits the case against the memory budget and sizes the hot (1) or rotating-cold ring;
   3. tunes (hot: autotuned launcher; cold: rotating-ring tuner over fixed candidates);
@@ -24,6 +26,7 @@ from kernels.grouped_gemm import (
     grouped_candidate_configs,
     launch_grouped,
 )
+from kernels.grouped_mm import build_offsets_workspace, launch_grouped_offsets
 from kernels.matmul import select_config
 from kernels.torch_grouped_gemm import (
     TorchGroupedMMUnavailable,
@@ -48,8 +51,8 @@ _TABLE_BYTES_PER_PROBLEM = 3 * 8 + 3 * 4 + 6 * 8  # pointer tables, dims, stride
 
 
 def _estimate(shapes: list[tuple[int, int, int]], item_size: int, mode: str) -> int:
-    """Bytes one workspace of this case needs (torch mode pads row strides to 16 bytes)."""
-    if mode == "torch":
+    """Bytes one workspace of this case needs (torch and offsets modes pad row strides to 16 bytes)."""
+    if mode in ("torch", "offsets"):
         step = max(1, 16 // item_size)
         pad = lambda v: -(-v // step) * step  # noqa: E731
         return sum(item_size * (m * pad(k) + k * pad(n) + m * pad(n)) for m, k, n in shapes) + 4 * len(shapes)
@@ -126,9 +129,12 @@ def _build_ring(args, shapes, projection: str, mode: str, ring: int, minimum: in
     cfg = select_config(shapes[0][0], shapes[0][2], shapes[0][1], dtype)
     while ring >= minimum:
         try:
+            operation = "gate_up" if projection == "W1" else "down"
             if mode == "torch":
-                operation = "gate_up" if projection == "W1" else "down"
                 return [build_torch_grouped_workspace(shapes, dtype, args.seed + i * 100003, operation=operation)
+                        for i in range(ring)], ring
+            if mode == "offsets":
+                return [build_offsets_workspace(shapes, dtype, args.seed + i * 100003, operation=operation)
                         for i in range(ring)], ring
             builder = build_fused_gate_up_workspace if projection == "W1" else build_grouped_workspace
             return [builder(shapes, dtype, args.seed + i * 100003, cfg) for i in range(ring)], ring
@@ -146,6 +152,17 @@ def _reference(a, b, projection: str):
         return torch.cat((torch.matmul(a.float(), b[:, :half].float()),
                           torch.matmul(a.float(), b[:, half:].float())), dim=1).to(a.dtype)
     return torch.matmul(a.float(), b.float()).to(a.dtype)
+
+
+def _launch_hip(workspace, mode: str, precision: str, cfg, autotune: bool) -> None:
+    if mode == "offsets":
+        launch_grouped_offsets(workspace, precision, cfg, autotune=autotune)
+    else:
+        launch_grouped(workspace, precision, cfg, autotune=autotune)
+
+
+def _outputs(workspace, mode: str):
+    return [workspace.output] if mode == "offsets" else workspace.c
 
 
 def _run_case(args, env: dict[str, Any], projection: str, parallel_type: str, mode: str, m: int) -> dict[str, Any]:
@@ -191,22 +208,22 @@ def _run_case(args, env: dict[str, Any], projection: str, parallel_type: str, mo
                 max(s[0] for s in shapes), max(s[2] for s in shapes), max(s[1] for s in shapes),
                 problem_count=len(shapes), sm_count=workspaces[0].sm_count, dtype=torch_dtype(args.dtype))
             tuning = tune_rotating_configs(
-                candidates, lambda c, i: launch_grouped(workspaces[i % ring], args.input_precision, c, autotune=False),
+                candidates, lambda c, i: _launch_hip(workspaces[i % ring], mode, args.input_precision, c, False),
                 ring)
             cfg = tuning.config
         hot = args.cache_mode == "hot"
         for workspace in workspaces:
-            if mode == "grouped":
-                launch_grouped(workspace, args.input_precision, cfg, autotune=hot)
-            else:
+            if mode == "torch":
                 launch_torch_grouped(workspace)
+            else:
+                _launch_hip(workspace, mode, args.input_precision, cfg, hot)
         torch.cuda.synchronize()
-        if mode == "grouped":
+        if mode != "torch":
             # Tuning wrote C with several candidates: poison it and run the winner alone.
             for workspace in workspaces:
-                for output in workspace.c:
+                for output in _outputs(workspace, mode):
                     output.fill_(float("nan"))
-                launch_grouped(workspace, args.input_precision, workspace.config, autotune=False)
+                _launch_hip(workspace, mode, args.input_precision, workspace.config, False)
             torch.cuda.synchronize()
         max_abs = max_rel = 0.0
         for workspace in workspaces:
@@ -214,7 +231,7 @@ def _run_case(args, env: dict[str, Any], projection: str, parallel_type: str, mo
                 abs_err, rel_err = assert_close(c, _reference(a, b, projection), args.dtype)
                 max_abs, max_rel = max(max_abs, abs_err), max(max_rel, rel_err)
         row["workspace_bytes"] = sum(w.storage_bytes for w in workspaces)
-        if mode == "grouped":
+        if mode != "torch":
             cfg = workspaces[0].config
             row.update(
                 block_m=cfg.block_m, block_n=cfg.block_n, block_k=cfg.block_k, group_size_m=cfg.group_size_m,
@@ -232,10 +249,10 @@ def _run_case(args, env: dict[str, Any], projection: str, parallel_type: str, mo
 
         def invoke(index: int) -> None:
             current = workspaces[index % ring]
-            if mode == "grouped":
-                launch_grouped(current, args.input_precision, cfg, autotune=hot)
-            else:
+            if mode == "torch":
                 launch_torch_grouped(current)
+            else:
+                _launch_hip(current, mode, args.input_precision, cfg, hot)
 
         timing = time_cuda(invoke, args.warmup, args.repeat, args.target_timing_ms, workspace_count=ring)
         tflops = total / (timing.median_ms * 1e9)
@@ -279,7 +296,8 @@ def run_moe(args, env: dict[str, Any]) -> dict[str, list[dict[str, Any]]]:
     if nonintegral:
         raise ValueError("M*num_experts must be divisible by topk so T is integral; invalid M values: "
                          + ",".join(map(str, nonintegral)))
-    modes = ["grouped"] + (["torch"] if args.torch_baseline else [])
+    modes = (["grouped"] + (["offsets"] if getattr(args, "offsets_layout", False) else [])
+             + (["torch"] if args.torch_baseline else []))
     outputs: dict[str, list[dict[str, Any]]] = {"W1": [], "W2": []}
     for projection in ("W1", "W2"):
         for m in ms:

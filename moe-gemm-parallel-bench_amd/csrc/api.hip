@@ -5,6 +5,7 @@
 // stream (capturable in a HIP graph) or an error code with a message in moegemm_last_error().
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -158,6 +159,56 @@ int moegemm_grouped_gemm(const int64_t* a_ptrs, const int64_t* b_ptrs, const int
   if (p.total_tiles == 0) return MOEGEMM_OK;
   int grid = grid_size <= 0 ? p.total_tiles : (grid_size < p.total_tiles ? grid_size : p.total_tiles);
   return launch(e, p, grid, vector_layout != 0, stream);
+}
+
+int moegemm_grouped_mm_offs(const void* a, const void* b, void* c, const int32_t* offs, int32_t group_count,
+                            int32_t rows, int32_t n, int32_t k, int64_t stride_am, int64_t stride_bg,
+                            int64_t stride_bk, int64_t stride_cm, int32_t dtype, int32_t input_precision,
+                            int32_t block_m, int32_t block_n, int32_t block_k, int32_t group_size_m,
+                            int32_t num_warps, int32_t num_stages, int32_t grid_size, void* stream) {
+  const KernelEntry* e = nullptr;
+  int rc = check_common(dtype, input_precision, group_size_m, &e, block_m, block_n, block_k, num_warps, num_stages);
+  if (rc != MOEGEMM_OK) return rc;
+  if (!a || !b || !c || !offs) return fail(MOEGEMM_ERR_INVALID, "matrix and offsets pointers must be non-null");
+  if (group_count <= 0) return fail(MOEGEMM_ERR_INVALID, "group_count must be positive (got %d)", group_count);
+  if (rows < 0 || n <= 0 || k <= 0)
+    return fail(MOEGEMM_ERR_INVALID, "shape must have rows >= 0 and positive n, k (rows=%d n=%d k=%d)", rows, n, k);
+  if (stride_am < k || stride_bk < n || stride_cm < n || stride_bg < (int64_t)k * stride_bk)
+    return fail(MOEGEMM_ERR_INVALID,
+                "strides overlap rows or groups (stride_am=%lld stride_bk=%lld stride_bg=%lld stride_cm=%lld)",
+                (long long)stride_am, (long long)stride_bk, (long long)stride_bg, (long long)stride_cm);
+  if (rows == 0) return MOEGEMM_OK;
+  // Upper bound on the tile count: every group adds at most one partial M tile.
+  const int64_t m_tiles = std::min<int64_t>(rows / block_m + group_count, (int64_t)group_count * cdiv(rows, block_m));
+  const int64_t tiles = m_tiles * cdiv(n, block_n);
+  if (tiles > INT32_MAX) return fail(MOEGEMM_ERR_INVALID, "tile bound %lld exceeds int32", (long long)tiles);
+  KParams p;
+  std::memset(&p, 0, sizeof(p));
+  p.mode = MODE_OFFSETS;
+  p.a = a;
+  p.b = b;
+  p.c = c;
+  p.offs = offs;
+  p.G = group_count;
+  p.rows = rows;
+  p.N = n;
+  p.K = k;
+  p.sam = stride_am;
+  p.sbk = stride_bk;
+  p.sbg = stride_bg;
+  p.scm = stride_cm;
+  p.group_m = group_size_m;
+  p.tf32 = input_precision == MOEGEMM_PRECISION_TF32;
+  p.total_tiles = (int32_t)tiles;
+  const int grid = grid_size <= 0 ? p.total_tiles : (grid_size < p.total_tiles ? grid_size : p.total_tiles);
+  // Every group shares the strides, so one check covers all of them; the A resource of a tile spans
+  // at most block_m rows, each group's B resource one [k, n] panel.
+  const bool vec = (dtype == DT_BF16 || dtype == DT_F16) && k % 8 == 0 && n % 8 == 0 && stride_am % 8 == 0 &&
+                   stride_bk % 8 == 0 && stride_bg % 8 == 0 && stride_cm % 4 == 0 &&
+                   (reinterpret_cast<uintptr_t>(a) & 15) == 0 && (reinterpret_cast<uintptr_t>(b) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(c) & 7) == 0 && (int64_t)block_m * stride_am * 2 < (int64_t(1) << 31) &&
+                   (int64_t)k * stride_bk * 2 < (int64_t(1) << 31);
+  return launch(e, p, grid, vec, stream);
 }
 
 int moegemm_matmul(const void* a, const void* b, void* c, int32_t m, int32_t n, int32_t k, int64_t stride_am,

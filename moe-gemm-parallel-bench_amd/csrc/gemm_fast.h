@@ -69,6 +69,7 @@ template <class E, int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_>
 struct FastTile {
   static_assert(!E::is_f32, "the DMA fast path is for 16-bit operands");
   static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, STAGES = STAGES_;
+  static constexpr int ES = 2;  // element size in bytes
   static constexpr int NW = WM * WN;
   static constexpr int NT = NW * 64;
   static constexpr int WTM = BM / WM;

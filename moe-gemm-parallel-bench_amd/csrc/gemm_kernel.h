@@ -21,6 +21,11 @@
 //    contiguous run of tiles per round; neighbouring tiles share A/B panels in that XCD's L2.
 //  * Generic groups (heterogeneous shapes/strides) map tile -> problem with an LDS prefix sum of
 //    per-problem tile counts and a binary search, instead of a per-tile scan over all problems.
+//  * Offsets mode (the expert-sorted layout of torch.nn.functional.grouped_mm: A [rows, K] and
+//    C [rows, N] split by cumulative int32 end rows `offs`, B [G, K, N]) derives each group's row
+//    count from `offs` on the device, so a router can produce `offs` without a host round trip;
+//    the host passes only an upper bound on the tile count and the grid stops at the device total.
+//    Offsets are clamped to [0, rows], so no access leaves A or C whatever `offs` holds.
 //  * Every problem is checked at run time for the vector preconditions (unit inner stride, row
 //    stride and extent multiples of the 16-byte chunk, 16-byte aligned base); a problem that fails
 //    them is staged element by element with arbitrary strides.  Pointer tables are read from
@@ -42,7 +47,7 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 enum DType : int { DT_F16 = 0, DT_BF16 = 1, DT_F32 = 2 };
-enum Mode : int { MODE_SINGLE = 0, MODE_HOMOGENEOUS = 1, MODE_GENERIC = 2 };
+enum Mode : int { MODE_SINGLE = 0, MODE_HOMOGENEOUS = 1, MODE_GENERIC = 2, MODE_OFFSETS = 3 };
 
 // Kernel arguments, passed by value.  Strides are in elements.
 struct KParams {
@@ -54,7 +59,10 @@ struct KParams {
   const void* a;           // single mode operands
   const void* b;
   void* c;
-  int64_t sam, sak, sbk, sbn, scm, scn;  // single mode strides
+  int64_t sam, sak, sbk, sbn, scm, scn;  // single / offsets mode strides
+  const int32_t* offs;   // offsets mode: [G] cumulative end rows of the expert-sorted A and C
+  int64_t sbg;           // offsets mode: B stride between groups (elements)
+  int32_t rows;          // offsets mode: rows of A and C; offsets are clamped to it
   int32_t mode;
   int32_t G;
   int32_t M, N, K;       // single / homogeneous shape
@@ -479,7 +487,17 @@ __device__ __forceinline__ void group_m_order(int local, int m_tiles, int n_tile
   tn = (local % width) / gsz;
 }
 
-// Generic mode: s_pref[i] = tile offset of problem first+i, for one chunk of PREFIX problems.
+// Offsets mode: first row and row count of group e, with the offsets clamped to [0, rows] and a
+// decreasing offset read as an empty group.
+__device__ __forceinline__ int offsets_rows(const KParams& p, int e, int& m) {
+  const int lo = e == 0 ? 0 : min(max(p.offs[e - 1], 0), p.rows);
+  const int hi = min(max(p.offs[e], 0), p.rows);
+  m = hi > lo ? hi - lo : 0;
+  return lo;
+}
+
+// Generic and offsets modes: s_pref[i] = tile offset of problem first+i, for one chunk of PREFIX
+// problems.
 template <class T>
 __device__ __forceinline__ void load_prefix(const KParams& p, int* s_pref, int* s_tot, int first, int base) {
   constexpr int PER = (T::PREFIX + T::NT - 1) / T::NT;
@@ -491,7 +509,14 @@ __device__ __forceinline__ void load_prefix(const KParams& p, int* s_pref, int* 
     const int prob = first + i;
     int cnt = 0;
     if (i < T::PREFIX && prob < p.G) {
-      const int m = p.dims[prob * 3 + 0], n = p.dims[prob * 3 + 1];
+      int m, n;
+      if (p.mode == MODE_OFFSETS) {
+        offsets_rows(p, prob, m);
+        n = p.N;
+      } else {
+        m = p.dims[prob * 3 + 0];
+        n = p.dims[prob * 3 + 1];
+      }
       cnt = (m > 0 && n > 0) ? ((m + T::BM - 1) / T::BM) * ((n + T::BN - 1) / T::BN) : 0;
     }
     local += cnt;
@@ -526,7 +551,8 @@ __global__ void __launch_bounds__(T::NT) grouped_gemm_kernel(KParams p) {
   if ((grid & 7) == 0) vid = (blockIdx.x & 7) * (grid >> 3) + (blockIdx.x >> 3);
 
   int chunk_first = 0;
-  if (p.mode == MODE_GENERIC) load_prefix<T>(p, s_pref, s_tot, 0, 0);
+  const bool searched = p.mode == MODE_GENERIC || p.mode == MODE_OFFSETS;
+  if (searched) load_prefix<T>(p, s_pref, s_tot, 0, 0);
 
   for (int t = vid; t < p.total_tiles; t += grid) {
     ProblemDesc pd;
@@ -565,14 +591,25 @@ __global__ void __launch_bounds__(T::NT) grouped_gemm_kernel(KParams p) {
       }
       const int e = uniform(chunk_first + lo);
       const int local = uniform(t - s_pref[lo]);
-      pd.m = p.dims[e * 3 + 0]; pd.n = p.dims[e * 3 + 1]; pd.k = p.dims[e * 3 + 2];
+      if (p.mode == MODE_OFFSETS) {
+        int m;
+        const int row0 = uniform(offsets_rows(p, e, m));
+        pd.m = uniform(m); pd.n = p.N; pd.k = p.K;
+        pd.sam = p.sam; pd.sak = 1; pd.sbk = p.sbk; pd.sbn = 1; pd.scm = p.scm; pd.scn = 1;
+        constexpr int ES = T::ES;
+        pd.a = static_cast<const char*>(p.a) + (int64_t)row0 * p.sam * ES;
+        pd.b = static_cast<const char*>(p.b) + (int64_t)e * p.sbg * ES;
+        pd.c = static_cast<char*>(p.c) + (int64_t)row0 * p.scm * ES;
+      } else {
+        pd.m = p.dims[e * 3 + 0]; pd.n = p.dims[e * 3 + 1]; pd.k = p.dims[e * 3 + 2];
+        const int64_t* s = p.strides + (int64_t)e * 6;
+        pd.sam = s[0]; pd.sak = s[1]; pd.sbk = s[2]; pd.sbn = s[3]; pd.scm = s[4]; pd.scn = s[5];
+        pd.a = reinterpret_cast<const char*>(p.a_ptrs[e]);
+        pd.b = reinterpret_cast<const char*>(p.b_ptrs[e]);
+        pd.c = reinterpret_cast<char*>(p.c_ptrs[e]);
+      }
       const int mt = (pd.m + T::BM - 1) / T::BM, nt = (pd.n + T::BN - 1) / T::BN;
       group_m_order(local, mt, nt, p.group_m, tm, tn);
-      const int64_t* s = p.strides + (int64_t)e * 6;
-      pd.sam = s[0]; pd.sak = s[1]; pd.sbk = s[2]; pd.sbn = s[3]; pd.scm = s[4]; pd.scn = s[5];
-      pd.a = reinterpret_cast<const char*>(p.a_ptrs[e]);
-      pd.b = reinterpret_cast<const char*>(p.b_ptrs[e]);
-      pd.c = reinterpret_cast<char*>(p.c_ptrs[e]);
     }
     make_uniform(pd);
     T::run_tile(pd, uniform(tm), uniform(tn), smem, p.tf32 != 0);

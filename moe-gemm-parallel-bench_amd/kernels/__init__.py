@@ -7,6 +7,13 @@ from .grouped_gemm import (
     grouped_candidate_configs,
     launch_grouped,
 )
+from .grouped_mm import (
+    OffsetsWorkspace,
+    build_offsets_workspace,
+    grouped_mm,
+    last_grouped_mm_config,
+    launch_grouped_offsets,
+)
 from .matmul import (
     KernelConfig,
     last_matmul_config,
@@ -25,14 +32,19 @@ from .torch_grouped_gemm import (
 __all__ = [
     "GroupedWorkspace",
     "KernelConfig",
+    "OffsetsWorkspace",
     "TorchGroupedMMUnavailable",
     "TorchGroupedWorkspace",
     "build_fused_gate_up_workspace",
     "build_grouped_workspace",
+    "build_offsets_workspace",
     "build_torch_grouped_workspace",
     "grouped_candidate_configs",
+    "grouped_mm",
+    "last_grouped_mm_config",
     "last_matmul_config",
     "launch_grouped",
+    "launch_grouped_offsets",
     "launch_matmul",
     "launch_torch_grouped",
     "matmul_candidate_configs",

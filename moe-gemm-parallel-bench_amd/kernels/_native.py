@@ -15,7 +15,7 @@ from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().with_name("libmoegemm.so")
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 OK = 0
 ERR_INVALID = -1
 ERR_NO_KERNEL = -2
@@ -43,6 +43,11 @@ SIGNATURES = {
         ctypes.c_int,
         [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
          _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
+    ),
+    "moegemm_grouped_mm_offs": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i32, _i32,
+         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
     ),
     "moegemm_matmul": (
         ctypes.c_int,

@@ -1,0 +1,216 @@
+"""Expert-sorted grouped GEMM (2-D A, 3-D B, int32 offsets) on gfx950.
+
+The layout a router produces after token permutation: one expert-sorted A [rows, K], the expert
+weights as one B [G, K, N], and int32 cumulative end rows ``offs`` [G], so that group e owns rows
+offs[e-1]:offs[e] of A and C.  This is the operand layout of the reference's torch provider
+(kernels/torch_grouped_gemm.py:121-174: ``build_torch_grouped_workspace`` pads row strides to 16 B
+and calls ``torch.nn.functional.grouped_mm(mat_a, mat_b, offs=offs)`` once).  Here the same
+operands go to the persistent HIP kernel through ``moegemm_grouped_mm_offs``:
+
+* ``grouped_mm(mat_a, mat_b, offs, out=None)`` has the 2-D x 3-D semantics of
+  ``torch.nn.functional.grouped_mm`` (C[offs[e-1]:offs[e]] = A[offs[e-1]:offs[e]] @ B[e], fp32
+  accumulation, output in the operand dtype).  ``offs`` stays on the device: the kernel derives
+  every group's row count from it at run time, so the call needs no host synchronisation and is
+  capturable in a HIP graph (one kernel launch).  Rows at or past offs[-1] are not written (torch
+  leaves them unspecified too: ``out=None`` allocates with ``torch.empty`` like torch); offsets
+  beyond ``rows`` are clamped on the device, so any ``offs`` content is memory-safe (offsets that
+  decrease give empty or overlapping groups, whose results are unspecified).
+* ``build_offsets_workspace`` / ``launch_grouped_offsets`` mirror the torch provider's workspace
+  API for the drivers (same seeded ``normal_() * 0.1`` operands, same 16-byte row padding, same
+  ``problem_tensors()`` view of each expert).
+"""
+
+from __future__ import annotations
+
+from collections.abc import Iterator, Sequence
+from dataclasses import dataclass
+from itertools import accumulate
+
+from . import _native
+from .grouped_gemm import grouped_candidate_configs
+from .matmul import KernelConfig, _device_signature, _require_runtime, _tune, select_config
+
+
+def offsets_tile_bound(rows: int, group_count: int, n: int, block_m: int, block_n: int) -> int:
+    """Host-side upper bound of the tile count the kernel may find in ``offs`` (mirrors the C ABI).
+
+    Each group contributes at most one partial M tile, and no group has more rows than A.
+    """
+    if rows <= 0:
+        return 0
+    m_tiles = min(rows // block_m + group_count, group_count * -(-rows // block_m))
+    return m_tiles * -(-n // block_n)
+
+
+def _validate(mat_a, mat_b, offs, out):
+    import torch
+
+    if mat_a.ndim != 2 or mat_b.ndim != 3:
+        raise ValueError("grouped_mm expects a 2-D mat_a [rows, K] and a 3-D mat_b [G, K, N]")
+    rows, k = mat_a.shape
+    groups, kb, n = mat_b.shape
+    if k != kb:
+        raise ValueError(f"contraction mismatch: mat_a K={k}, mat_b K={kb}")
+    if offs.ndim != 1 or offs.dtype != torch.int32 or offs.shape[0] != groups:
+        raise ValueError(f"offs must be an int32 vector with one entry per group ({groups})")
+    if groups <= 0 or k <= 0 or n <= 0:
+        raise ValueError("grouped_mm needs at least one group and positive K and N")
+    devices = {mat_a.device, mat_b.device, offs.device}
+    if out is not None:
+        devices.add(out.device)
+    if len(devices) != 1 or mat_a.device.type != "cuda":
+        raise ValueError("mat_a, mat_b, offs and out must be on the same GPU device")
+    if mat_a.dtype != mat_b.dtype:
+        raise ValueError("mat_a and mat_b must have the same dtype")
+    if mat_a.stride(1) != 1 or mat_b.stride(2) != 1:
+        raise ValueError("mat_a and mat_b need a unit stride along their last dimension")
+    if out is not None:
+        if tuple(out.shape) != (rows, n) or out.dtype != mat_a.dtype or out.stride(1) != 1:
+            raise ValueError(f"out must be a [{rows}, {n}] {mat_a.dtype} matrix with unit column stride")
+    return int(rows), int(k), int(n), int(groups)
+
+
+def _launch_fixed(mat_a, mat_b, offs, out, rows, k, n, groups, cfg: KernelConfig, dtype_code: int,
+                  precision: int, sm_count: int) -> None:
+    grid = max(1, min(offsets_tile_bound(rows, groups, n, cfg.block_m, cfg.block_n), sm_count * cfg.cta_multiplier))
+    status = _native.library().moegemm_grouped_mm_offs(
+        mat_a.data_ptr(), mat_b.data_ptr(), out.data_ptr(), offs.data_ptr(), groups, rows, n, k,
+        mat_a.stride(0), mat_b.stride(0), mat_b.stride(1), out.stride(0), dtype_code, precision,
+        cfg.block_m, cfg.block_n, cfg.block_k, cfg.group_size_m, cfg.num_warps, cfg.num_stages, grid,
+        _native.current_stream_handle(mat_a.device),
+    )
+    _native.check(status)
+
+
+_OFFSETS_AUTOTUNE_CACHE: dict[tuple, KernelConfig] = {}
+_LAST_CONFIG: list[KernelConfig | None] = [None]
+
+
+def last_grouped_mm_config() -> KernelConfig | None:
+    """Config used by the most recent ``grouped_mm`` call."""
+    return _LAST_CONFIG[0]
+
+
+def grouped_mm(mat_a, mat_b, offs, *, out=None, config: KernelConfig | None = None,
+               input_precision: str = "ieee", autotune: bool = True):
+    """C = per-group A @ B[e] over the expert-sorted layout; returns ``out`` (allocated if None).
+
+    With ``autotune=True`` and no ``config``, the first call per (rows, K, N, G, strides, dtype)
+    key measures the candidate tiles on these operands; later calls are a cache lookup plus one
+    kernel launch.  The tuning key does not include ``offs``: the candidates are ranked for an
+    even split of ``rows`` over the groups.
+    """
+    import torch
+
+    rows, k, n, groups = _validate(mat_a, mat_b, offs, out)
+    _require_runtime()
+    if out is None:
+        out = torch.empty((rows, n), device=mat_a.device, dtype=mat_a.dtype)
+    if rows == 0:
+        return out
+    dtype_code = _native.dtype_code(mat_a.dtype)
+    precision = _native.precision_code(input_precision, dtype_code)
+    sm_count = _device_signature(mat_a.device) % 1000
+    mean_m = max(1, rows // groups)
+
+    def launch(cfg):
+        _launch_fixed(mat_a, mat_b, offs, out, rows, k, n, groups, cfg, dtype_code, precision, sm_count)
+
+    if config is not None or not autotune:
+        cfg = config or select_config(mean_m, n, k, mat_a.dtype)
+    else:
+        key = (rows, k, n, groups, tuple(mat_a.stride()), tuple(mat_b.stride()), tuple(out.stride()),
+               dtype_code, precision, _device_signature(mat_a.device))
+        cfg = _OFFSETS_AUTOTUNE_CACHE.get(key)
+        if cfg is None:
+            candidates = grouped_candidate_configs(mean_m, n, k, problem_count=max(groups, 2), sm_count=sm_count,
+                                                   dtype=mat_a.dtype)
+            cfg = _tune(candidates, launch)
+            _OFFSETS_AUTOTUNE_CACHE[key] = cfg
+    launch(cfg)
+    _LAST_CONFIG[0] = cfg
+    return out
+
+
+@dataclass
+class OffsetsWorkspace:
+    mat_a: object
+    mat_b: object
+    offs: object
+    shapes: tuple[tuple[int, int, int], ...]
+    output: object
+    config: KernelConfig
+    sm_count: int = 0
+    device_signature: int = 0
+    operation: str = "gemm"
+    scheduler: str = "not_launched"
+
+    @property
+    def problem_count(self) -> int:
+        return len(self.shapes)
+
+    @property
+    def storage_bytes(self) -> int:
+        tensors = (self.mat_a, self.mat_b, self.offs, self.output)
+        return sum(t.untyped_storage().nbytes() for t in tensors)
+
+    def problem_tensors(self) -> Iterator[tuple[object, object, object]]:
+        row = 0
+        for index, (m, _, _) in enumerate(self.shapes):
+            yield self.mat_a[row:row + m], self.mat_b[index], self.output[row:row + m]
+            row += m
+
+
+def build_offsets_workspace(
+    shapes: Sequence[tuple[int, int, int]],
+    dtype,
+    seed: int = 0,
+    *,
+    operation: str = "gemm",
+    device: str = "cuda",
+) -> OffsetsWorkspace:
+    """Expert-sorted operands for (M_e, K, N) problems sharing K and N (16-byte padded rows)."""
+    import torch
+
+    if not shapes:
+        raise ValueError("grouped GEMM requires at least one problem")
+    normalized = tuple(tuple(int(v) for v in s) for s in shapes)
+    if any(len(s) != 3 or s[0] < 0 or s[1] <= 0 or s[2] <= 0 for s in normalized):
+        raise ValueError("every shape must be an (M >= 0, K > 0, N > 0) triple")
+    _, k, n = normalized[0]
+    if any(kk != k or nn != n for _, kk, nn in normalized):
+        raise ValueError("the expert-sorted layout requires shared K and N dimensions")
+    ends = tuple(accumulate(m for m, _, _ in normalized))
+    if ends[-1] > 2**31 - 1:
+        raise ValueError("offsets exceed int32 range")
+    per16 = max(1, 16 // torch.empty((), dtype=dtype).element_size())
+
+    def padded(extent: int) -> int:
+        return -(-extent // per16) * per16
+
+    generator = torch.Generator(device=device).manual_seed(seed)
+    rows = ends[-1]
+    mat_a = torch.empty((rows, padded(k)), device=device, dtype=dtype)[:, :k]
+    mat_b = torch.empty((len(normalized), k, padded(n)), device=device, dtype=dtype)[:, :, :n]
+    mat_a.normal_(generator=generator).mul_(0.1)
+    mat_b.normal_(generator=generator).mul_(0.1)
+    output = torch.empty((rows, padded(n)), device=device, dtype=dtype)[:, :n]
+    offs = torch.tensor(ends, device=device, dtype=torch.int32)
+    config = select_config(max(1, rows // len(normalized)), n, k, dtype)
+    signature = _device_signature(mat_a.device) if mat_a.device.type == "cuda" else 0
+    return OffsetsWorkspace(mat_a, mat_b, offs, normalized, output, config, sm_count=signature % 1000,
+                            device_signature=signature, operation=operation)
+
+
+def launch_grouped_offsets(workspace: OffsetsWorkspace, input_precision: str = "ieee",
+                           config: KernelConfig | None = None, *, autotune: bool = True) -> None:
+    """One persistent kernel over the workspace; records the config used and the scheduler name.
+
+    Like ``launch_grouped``: with ``autotune=True`` the per-workload tuner picks the config (an
+    explicit ``config`` is ignored); otherwise ``config`` (or the workspace's) runs as given.
+    """
+    grouped_mm(workspace.mat_a, workspace.mat_b, workspace.offs, out=workspace.output,
+               config=None if autotune else (config or workspace.config),
+               input_precision=input_precision, autotune=autotune)
+    workspace.config = last_grouped_mm_config()
+    workspace.scheduler = "offsets_persistent"

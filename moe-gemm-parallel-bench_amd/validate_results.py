@@ -21,6 +21,7 @@ from pathlib import Path
 from typing import Any
 
 SCHEDULERS = {"homogeneous_persistent", "generic_persistent", "single_problem_matmul"}
+OFFSETS_SCHEDULER = "offsets_persistent"  # the HIP kernel over the expert-sorted (offsets) layout
 EXPERIMENT_FILES = {
     "shapes": ["gemm_shape_sweep.csv"],
     "moe": ["moe_w1.csv", "moe_w2.csv"],
@@ -73,14 +74,15 @@ def _moe_execution_contract_valid(row: dict[str, str]) -> bool:
             and _truthy(row.get("execution_verified"))
             and _falsey(row.get("output_preallocated"))
         )
-    if mode != "grouped":
+    if mode not in ("grouped", "offsets"):
         return False
+    schedulers = SCHEDULERS if mode == "grouped" else {OFFSETS_SCHEDULER}
     tile_fields = ("block_m", "block_n", "block_k", "num_warps", "num_stages", "cta_multiplier")
     return (
         _truthy(row.get("autotune_enabled"))
         and row.get("autotune_status") == "selected"
         and row.get("config_source") in {"workload_autotune", "cold_ring_autotune"}
-        and row.get("scheduler") in SCHEDULERS
+        and row.get("scheduler") in schedulers
         and row.get("launches_per_iteration") == "1"
         and _truthy(row.get("output_preallocated"))
         and all(_positive_integer(row.get(field)) for field in tile_fields)

@@ -19,6 +19,14 @@ Functions and the reference code they restate:
   * ``tile_order``                  kernels/grouped_gemm.py:353-360 (GROUP_M traversal + persistent
                                     stride); pinned by a coverage/bijection check.
   * ``w13_reference``               benchmark_moe.py:258-266 (cat of gate and up products).
+  * ``offsets_groups`` / ``grouped_mm_offsets``  the expert-sorted 2-D A / 3-D B / int32 ``offs``
+                                    layout of kernels/torch_grouped_gemm.py:139-158 with the
+                                    semantics of torch.nn.functional.grouped_mm (group e owns rows
+                                    offs[e-1]:offs[e]; rows past offs[-1] are unspecified there and
+                                    zero here); pinned against
+                                    torch's CPU grouped_mm and a brute force in tests/test_oracle.py.
+  * ``offsets_tile_bound``          the host's tile-count bound for that layout (each group adds at
+                                    most one partial M tile); pinned by exhaustive small cases.
   * ``to_bf16_bits`` / ``to_f16_bits``  round-to-nearest-even casts; pinned against torch/numpy.
 """
 
@@ -150,6 +158,38 @@ def w13_reference(a: np.ndarray, b: np.ndarray, dtype: str, **kwargs) -> np.ndar
     gate = gemm(a, np.ascontiguousarray(b[:, :half]), dtype, **kwargs)
     up = gemm(a, np.ascontiguousarray(b[:, half:]), dtype, **kwargs)
     return np.concatenate([gate, up], axis=1)
+
+
+def offsets_groups(offs, rows: int) -> list[tuple[int, int]]:
+    """(first row, row count) of each group: offsets clamped to [0, rows], decreasing = empty."""
+    groups = []
+    prev = 0
+    for end in (int(v) for v in offs):
+        lo, hi = min(max(prev, 0), rows), min(max(end, 0), rows)
+        groups.append((lo, max(hi - lo, 0)))
+        prev = end
+    return groups
+
+
+def grouped_mm_offsets(a: np.ndarray, b3: np.ndarray, offs, dtype: str, **kwargs) -> np.ndarray:
+    """C [rows, N] with C[r0:r0+m] = A[r0:r0+m] @ B[e] per group; rows no group covers are zero."""
+    rows, k = a.shape
+    groups, kb, n = b3.shape
+    if k != kb or len(offs) != groups:
+        raise ValueError("expert-sorted operands disagree on K or the group count")
+    store = np.float32 if dtype == "fp32" else np.uint16
+    c = np.zeros((rows, n), dtype=store)
+    for e, (r0, m) in enumerate(offsets_groups(offs, rows)):
+        if m:
+            c[r0:r0 + m] = gemm(a[r0:r0 + m], b3[e], dtype, **kwargs)
+    return c
+
+
+def offsets_tile_bound(rows: int, group_count: int, n: int, block_m: int, block_n: int) -> int:
+    if rows <= 0:
+        return 0
+    m_tiles = min(rows // block_m + group_count, group_count * math.ceil(rows / block_m))
+    return m_tiles * math.ceil(n / block_n)
 
 
 def gemm_fast_bf16(a_bits: np.ndarray, b_bits: np.ndarray, threads: int, dtype: str = "bf16") -> np.ndarray:

@@ -374,3 +374,58 @@ def test_validate_results_end_to_end(tmp_path):
     assert not report["valid"]
     write_rows(tmp_path / "moe_w2.csv", [_moe_row("EP", **down, status="error")])
     assert not validate_results(tmp_path, tmp_path / "plots")["valid"]
+
+
+def test_offsets_workspace_layout_on_cpu():
+    from kernels.grouped_mm import build_offsets_workspace, offsets_tile_bound
+    from oracle import oracle
+
+    ws = build_offsets_workspace([(17, 13, 31), (0, 13, 31), (5, 13, 31)], torch.bfloat16, seed=3, device="cpu")
+    assert ws.offs.dtype == torch.int32 and ws.offs.tolist() == [17, 17, 22]
+    assert ws.mat_a.shape == (22, 13) and ws.mat_b.shape == (3, 13, 31) and ws.output.shape == (22, 31)
+    assert ws.mat_a.stride(0) % 8 == 0 and ws.mat_b.stride(1) % 8 == 0 and ws.output.stride(0) % 8 == 0
+    assert [a.shape[0] for a, _, _ in ws.problem_tensors()] == [17, 0, 5]
+    for rows, groups, n, bm, bn in ((22, 3, 31, 16, 64), (0, 3, 31, 16, 64), (1000, 7, 300, 256, 256)):
+        assert offsets_tile_bound(rows, groups, n, bm, bn) == oracle.offsets_tile_bound(rows, groups, n, bm, bn)
+    with pytest.raises(ValueError):
+        build_offsets_workspace([(17, 13, 31), (17, 14, 31)], torch.bfloat16, device="cpu")
+    with pytest.raises(ValueError):
+        build_offsets_workspace([(-1, 13, 31)], torch.bfloat16, device="cpu")
+
+
+def test_grouped_mm_validates_before_touching_a_gpu():
+    from kernels.grouped_mm import grouped_mm
+
+    a = torch.zeros((8, 16), dtype=torch.bfloat16)
+    b = torch.zeros((2, 16, 8), dtype=torch.bfloat16)
+    offs = torch.tensor([4, 8], dtype=torch.int32)
+    with pytest.raises(ValueError):  # host tensors: the kernel path needs a GPU device
+        grouped_mm(a, b, offs)
+    with pytest.raises(ValueError):
+        grouped_mm(a, b, offs.long())
+    with pytest.raises(ValueError):
+        grouped_mm(a, b[:, :8], offs)
+
+
+def test_moe_offsets_mode_is_opt_in(tmp_path):
+    base = dict(num_experts=8, parallel_size=4, ffn_size=16, hidden_size=32, topk=1, moe_ms=[1],
+                tokens=None, torch_baseline=False, results_dir=tmp_path)
+    for flag, expected in ((False, {"grouped"}), (True, {"grouped", "offsets"})):
+        calls: list[str] = []
+
+        def fake_run_case(_args, _env, _projection, _parallel_type, mode, _m):
+            calls.append(mode)
+            return {"status": "skipped"}
+
+        with patch("benchmark_moe._run_case", side_effect=fake_run_case), patch("benchmark_moe.write_rows"):
+            run_moe(SimpleNamespace(**base, offsets_layout=flag), {})
+        assert set(calls) == expected
+    assert _estimate([(16, 13, 31)], 2, "offsets") == _estimate([(16, 13, 31)], 2, "torch")
+
+
+def test_offsets_rows_need_the_offsets_scheduler():
+    row = {**GROUPED_ROW, "mode": "offsets", "scheduler": "offsets_persistent"}
+    assert _moe_execution_contract_valid(row)
+    assert not _moe_execution_contract_valid({**row, "scheduler": "homogeneous_persistent"})
+    assert not _moe_execution_contract_valid({**GROUPED_ROW, "scheduler": "offsets_persistent"})
+    assert not _moe_execution_contract_valid({**row, "launches_per_iteration": "2"})

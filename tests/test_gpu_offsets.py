@@ -1,0 +1,195 @@
+"""GPU parity tests of the expert-sorted layout (2-D A, 3-D B, int32 offsets) through the C ABI.
+
+The checker is ``oracle.grouped_mm_offsets`` (pinned against torch's CPU grouped_mm in
+tests/test_oracle.py).  Exact integers are compared bit for bit; seeded random inputs use the
+normwise bound max|C - R| / max|R| (bf16 <= 1e-2, fp16 <= 2e-3, fp32 <= 1e-5).  Cases: ragged
+offsets with empty groups and rows past the last offset (which must stay untouched), every
+compiled 16-bit tile, more groups than one LDS prefix chunk, offsets past the end of A (clamped
+on the device), a DeepSeek-V3 EP W13 shard on sampled rows, and a captured graph replayed with
+offsets rewritten in place between replays (the kernel reads them at run time).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import DTYPE_NAME, from_oracle, normwise, to_oracle
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+NORMWISE = {"bf16": 1e-2, "fp16": 2e-3, "fp32": 1e-5}
+DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+
+
+@pytest.fixture(autouse=True)
+def _gpu_only():
+    if not torch.cuda.is_available():
+        pytest.skip("ROCm GPU unavailable")
+    torch.manual_seed(11)
+
+
+def _oracle(mat_a, mat_b, offs_list):
+    name = DTYPE_NAME[mat_a.dtype]
+    c = oracle.grouped_mm_offsets(np.ascontiguousarray(to_oracle(mat_a)), np.ascontiguousarray(to_oracle(mat_b)),
+                                  offs_list, name)
+    return from_oracle(c, name)
+
+
+def _operands(rows, k, n, groups, dtype, *, integer=False):
+    if integer:
+        mat_a = torch.ones((rows, k), device="cuda", dtype=dtype)
+        mat_b = torch.stack([torch.full((k, n), float(e + 1), device="cuda", dtype=dtype) for e in range(groups)])
+    else:
+        mat_a = torch.randn((rows, k), device="cuda", dtype=dtype) / math.sqrt(k)
+        mat_b = torch.randn((groups, k, n), device="cuda", dtype=dtype) / math.sqrt(k)
+    return mat_a, mat_b
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: DTYPE_NAME[d])
+def test_ragged_offsets_random_inputs(dtype):
+    from kernels.grouped_mm import grouped_mm
+
+    rows, k, n = 203, 136, 72
+    offs_list = [17, 17, 90, 91, 160]  # empty group, single-row group, rows 160..202 past the end
+    print(f"offsets ragged dtype={DTYPE_NAME[dtype]} rows={rows} k={k} n={n} offs={offs_list}", flush=True)
+    mat_a, mat_b = _operands(rows, k, n, len(offs_list), dtype)
+    offs = torch.tensor(offs_list, device="cuda", dtype=torch.int32)
+    out = torch.full((rows, n), float("nan"), device="cuda", dtype=dtype)
+    grouped_mm(mat_a, mat_b, offs, out=out)
+    torch.cuda.synchronize()
+    covered = offs_list[-1]
+    expected = _oracle(mat_a, mat_b, offs_list)
+    assert torch.isfinite(out[:covered]).all()
+    assert normwise(out[:covered], expected[:covered]) <= NORMWISE[DTYPE_NAME[dtype]]
+    assert torch.isnan(out[covered:]).all(), "rows past offs[-1] were written"
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: DTYPE_NAME[d])
+def test_exact_integers_every_compiled_tile(dtype):
+    from kernels import _native
+    from kernels.grouped_mm import grouped_mm
+    from kernels.matmul import KernelConfig
+
+    rows, k, n = 150, 96, 80
+    offs_list = [0, 33, 33, 120, 150]
+    mat_a, mat_b = _operands(rows, k, n, len(offs_list), dtype, integer=True)
+    offs = torch.tensor(offs_list, device="cuda", dtype=torch.int32)
+    expected = torch.empty((rows, n), dtype=torch.float64)
+    prev = 0
+    for e, end in enumerate(offs_list):
+        expected[prev:end] = float(k * (e + 1))
+        prev = end
+    for bm, bn, bk, warps, stages, *_ in _native.compiled_kernels(_native.dtype_code(dtype)):
+        cfg = KernelConfig(bm, bn, bk, 8, warps, stages, 1)
+        print(f"offsets exact dtype={DTYPE_NAME[dtype]} tile={cfg.tile_key}", flush=True)
+        out = torch.full((rows, n), float("nan"), device="cuda", dtype=dtype)
+        grouped_mm(mat_a, mat_b, offs, out=out, config=cfg)
+        torch.cuda.synchronize()
+        assert torch.equal(out.double().cpu(), expected), f"tile {cfg.tile_key}"
+
+
+def test_many_groups_cross_prefix_chunks_and_clamped_offsets():
+    from kernels.grouped_mm import grouped_mm
+    from kernels.matmul import KernelConfig
+
+    groups, k, n = 1300, 32, 48  # > 1024 groups: the device prefix sum spans several chunks
+    rng = np.random.default_rng(5)
+    sizes = rng.integers(0, 5, size=groups)
+    ends = np.cumsum(sizes).astype(np.int64)
+    rows = int(ends[-1])
+    mat_a, mat_b = _operands(rows, k, n, groups, torch.bfloat16, integer=True)
+    offs_list = [int(v) for v in ends]
+    offs = torch.tensor(offs_list, device="cuda", dtype=torch.int32)
+    expected = torch.empty((rows, n), dtype=torch.float64)
+    prev = 0
+    for e, end in enumerate(offs_list):
+        # B holds bf16(e + 1); k times it is exact in the fp32 accumulator
+        expected[prev:end] = k * float(torch.tensor(float(e + 1)).to(torch.bfloat16))
+        prev = end
+    for cfg in (KernelConfig(16, 64, 128, 8, 4, 4, 1), KernelConfig(64, 64, 64, 8, 4, 4, 1)):
+        print(f"offsets many groups G={groups} rows={rows} tile={cfg.tile_key}", flush=True)
+        out = torch.full((rows, n), float("nan"), device="cuda", dtype=torch.bfloat16)
+        grouped_mm(mat_a, mat_b, offs, out=out, config=cfg)
+        torch.cuda.synchronize()
+        # exact-integer values k*(e+1) exceed bf16's 8-bit mantissa; compare to their bf16 rounding
+        assert torch.equal(out.double().cpu(), expected.to(torch.bfloat16).double())
+    # Offsets past the end of A are clamped on the device: the last group ends at `rows`.
+    clamped = offs_list[:-1] + [rows + 1000]
+    offs.copy_(torch.tensor(clamped, dtype=torch.int32))
+    out = torch.full((rows, n), float("nan"), device="cuda", dtype=torch.bfloat16)
+    print("offsets clamped last offset", flush=True)
+    grouped_mm(mat_a, mat_b, offs, out=out, config=KernelConfig(16, 64, 128, 8, 4, 4, 1))
+    torch.cuda.synchronize()
+    assert torch.equal(out.double().cpu(), expected.to(torch.bfloat16).double())
+
+
+def test_dsv3_ep_w13_shard_sampled_rows():
+    from kernels.grouped_mm import build_offsets_workspace, launch_grouped_offsets
+
+    rng = np.random.default_rng(9)
+    sizes = [int(v) for v in rng.integers(300, 700, size=32)]  # ragged routing around M_e = 512
+    shapes = [(m, 7168, 4096) for m in sizes]
+    print(f"offsets DSV3 EP W13 rows={sum(sizes)}", flush=True)
+    ws = build_offsets_workspace(shapes, torch.bfloat16, seed=1234, operation="gate_up")
+    launch_grouped_offsets(ws)
+    torch.cuda.synchronize()
+    assert ws.scheduler == "offsets_persistent" and ws.config is not None
+    for index, (a_e, b_e, c_e) in enumerate(ws.problem_tensors()):
+        if index not in (0, 13, 31):
+            continue
+        rows = torch.tensor([0, a_e.shape[0] // 2, a_e.shape[0] - 1])
+        expected = a_e[rows].float() @ b_e.float()
+        got = c_e[rows].float()
+        assert normwise(got.cpu(), expected.cpu()) <= 1e-2
+
+
+def test_graph_replay_reads_offsets_at_run_time():
+    from kernels.grouped_mm import grouped_mm
+    from kernels.matmul import KernelConfig
+
+    rows, k, n, groups = 96, 64, 64, 3
+    mat_a, mat_b = _operands(rows, k, n, groups, torch.float16, integer=True)
+    offs = torch.tensor([10, 50, 96], device="cuda", dtype=torch.int32)
+    out = torch.zeros((rows, n), device="cuda", dtype=torch.float16)
+    cfg = KernelConfig(32, 128, 64, 8, 4, 4, 1)
+    grouped_mm(mat_a, mat_b, offs, out=out, config=cfg)  # warm outside capture
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            grouped_mm(mat_a, mat_b, offs, out=out, config=cfg)
+    torch.cuda.synchronize()
+    for offs_list in ([10, 50, 96], [40, 41, 96], [0, 0, 96], [96, 96, 96]):
+        print(f"offsets graph replay offs={offs_list}", flush=True)
+        offs.copy_(torch.tensor(offs_list, dtype=torch.int32))
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        expected = torch.empty((rows, n), dtype=torch.float64)
+        prev = 0
+        for e, end in enumerate(offs_list):
+            expected[prev:end] = float(k * (e + 1))
+            prev = end
+        assert torch.equal(out.double().cpu(), expected)
+
+
+def test_validation_errors():
+    from kernels.grouped_mm import grouped_mm
+
+    a = torch.zeros((8, 16), device="cuda", dtype=torch.bfloat16)
+    b = torch.zeros((2, 16, 8), device="cuda", dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        grouped_mm(a, b, torch.tensor([4, 8], device="cuda", dtype=torch.int64))
+    with pytest.raises(ValueError):
+        grouped_mm(a, b, torch.tensor([8], device="cuda", dtype=torch.int32))
+    with pytest.raises(ValueError):
+        grouped_mm(a, b[:, :8], torch.tensor([4, 8], device="cuda", dtype=torch.int32))
+    with pytest.raises(ValueError):
+        grouped_mm(a.t(), b, torch.tensor([4, 8], device="cuda", dtype=torch.int32))

@@ -215,3 +215,80 @@ def test_tile_order_visits_every_tile_once(group_m, grid):
                 for tm in range(math.ceil(m / 64)) for tn in range(math.ceil(n / 64))}
     assert len(flat) == len(expected) == oracle.tile_count(shapes, 64, 64)
     assert set(flat) == expected
+
+
+# --------------------------------------------------------------------------------------------
+# Expert-sorted layout (2-D A, 3-D B, int32 offsets)
+
+def _torch_cpu_grouped_mm(a_bits, b_bits, offs, dtype):
+    import torch
+
+    tdt = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[dtype]
+    if dtype == "fp32":
+        ta, tb = torch.from_numpy(np.ascontiguousarray(a_bits)), torch.from_numpy(np.ascontiguousarray(b_bits))
+    else:
+        ta = torch.from_numpy(np.ascontiguousarray(a_bits).view(np.int16)).view(tdt)
+        tb = torch.from_numpy(np.ascontiguousarray(b_bits).view(np.int16)).view(tdt)
+    out = torch.nn.functional.grouped_mm(ta, tb, offs=torch.tensor(offs, dtype=torch.int32))
+    return out.float().numpy().astype(np.float64)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16", "fp32"])
+def test_grouped_mm_offsets_matches_torch_cpu_grouped_mm(dtype):
+    rng = np.random.default_rng(7)
+    rows, k, n = 37, 48, 24
+    offs = [5, 5, 19, 30]  # an empty group and rows 30..36 past the last offset
+    af = rng.standard_normal((rows, k)).astype(np.float32) / math.sqrt(k)
+    bf = rng.standard_normal((len(offs), k, n)).astype(np.float32) / math.sqrt(k)
+    enc = {"bf16": oracle.to_bf16_bits, "fp16": oracle.to_f16_bits, "fp32": lambda x: x}[dtype]
+    a, b = enc(af), enc(bf)
+    ours = _values(oracle.grouped_mm_offsets(a, b, offs, dtype), dtype)
+    theirs = _torch_cpu_grouped_mm(a, b, offs, dtype)
+    # torch accumulates in float32, the oracle in float64: 16-bit outputs are at most one output
+    # rounding step apart; fp32 outputs differ by float32 accumulation error (k terms, normwise).
+    ulp = {"bf16": 2.0 ** -7, "fp16": 2.0 ** -10, "fp32": 2.0 ** -21}[dtype]
+    scale = float(np.abs(theirs[:30]).max())
+    atol = k * 2.0 ** -24 * scale if dtype == "fp32" else ulp * 1e-2
+    # Rows past offs[-1] are unspecified in torch (left uninitialised); the oracle leaves zeros.
+    np.testing.assert_allclose(ours[:30], theirs[:30], rtol=ulp, atol=atol)
+    assert np.all(ours[30:] == 0)
+
+
+def test_grouped_mm_offsets_brute_force_and_planted_shift():
+    rng = np.random.default_rng(3)
+    rows, k, n = 9, 5, 3
+    offs = [2, 6, 9]
+    a = rng.standard_normal((rows, k)).astype(np.float32)
+    b = rng.standard_normal((3, k, n)).astype(np.float32)
+    got = oracle.grouped_mm_offsets(a, b, offs, "fp32").astype(np.float64)
+    brute = np.zeros((rows, n))
+    starts = [0] + offs[:-1]
+    for e, (lo, hi) in enumerate(zip(starts, offs)):
+        for r in range(lo, hi):
+            for j in range(n):
+                brute[r, j] = math.fsum(float(a[r, t]) * float(b[e, t, j]) for t in range(k))
+    np.testing.assert_allclose(got, brute, rtol=1e-6, atol=1e-6)
+    shifted = oracle.grouped_mm_offsets(a, b, [3, 6, 9], "fp32").astype(np.float64)  # planted: one row moved
+    assert not np.allclose(shifted, brute, rtol=1e-6, atol=1e-6)
+
+
+def test_offsets_groups_clamps_into_the_matrix():
+    assert oracle.offsets_groups([3, 3, 7], 10) == [(0, 3), (3, 0), (3, 4)]
+    assert oracle.offsets_groups([4, 2, 15], 10) == [(0, 4), (4, 0), (2, 8)]
+    assert oracle.offsets_groups([-5, 20], 10) == [(0, 0), (0, 10)]
+    for offs in ([3, 3, 7], [4, 2, 15], [-5, 20], [12, 12]):
+        for lo, m in oracle.offsets_groups(offs, 10):
+            assert 0 <= lo and lo + m <= 10
+
+
+@pytest.mark.parametrize("block_m,block_n", [(16, 64), (64, 128), (256, 256)])
+def test_offsets_tile_bound_covers_every_split(block_m, block_n):
+    n = 300
+    for rows in range(0, 43, 7):
+        for groups in (1, 2, 3, 4):
+            bound = oracle.offsets_tile_bound(rows, groups, n, block_m, block_n)
+            # every monotone split of rows into `groups` pieces (exhaustive over cut points)
+            for cuts in itertools.combinations_with_replacement(range(rows + 1), groups - 1):
+                ends = list(cuts) + [rows]
+                tiles = sum(math.ceil(m / block_m) for _, m in oracle.offsets_groups(ends, rows)) * math.ceil(n / block_n)
+                assert tiles <= bound
