@@ -10,9 +10,10 @@
 * ``roofline`` prices that kernel against the dense bf16 MFMA peak (2.5 PFLOP/s); ``traffic`` is
   the measured HBM bytes per launch from profiles/ (rocprofv3 FETCH_SIZE + WRITE_SIZE, scaled by a
   copy-kernel calibration) or null when no such profile is committed.
-* ``cases`` adds the HBM-bound M_e = 8 EP case, the TP counterparts (EP/TP ratio) and the DSV3 W2
-  cases, each timed the same way and checked against a float32 torch reference on a sample of
-  experts.
+* ``cases`` adds the HBM-bound M_e = 8 EP case, the TP counterparts (EP/TP ratio), the DSV3 W2
+  cases and the headline with the SwiGLU activation fused into the epilogue (a labelled variant:
+  the reference times W13 without the activation), each timed the same way and checked against a
+  float32 torch reference on a sample of experts.
 * ``cpu_baseline`` times the CPU oracle's blocked fp32-accumulating GEMM on the host cores on a
   bounded sample of the same workload (rank 0, N = 1 only).
 """
@@ -125,6 +126,51 @@ def _case(projection: str, parallel_type: str, m: int, steps: int, warmup: int, 
     return row
 
 
+def _swiglu_case(m: int, steps: int, warmup: int, seed: int = 1234) -> dict:
+    """DSV3 EP W13 with the SwiGLU activation fused into the epilogue (labelled variant)."""
+    import torch
+
+    from kernels.grouped_gemm import launch_gate_up_swiglu
+    from utils.metrics import gemm_flops
+
+    workspace = _workspace("W1", "EP", m, seed)
+    outputs = launch_gate_up_swiglu(workspace)  # autotune (untimed) on a cache miss
+    for h in outputs:
+        h.fill_(float("nan"))
+    launch_gate_up_swiglu(workspace, workspace.swiglu_config, autotune=False)
+    torch.cuda.synchronize()
+    f = workspace.shapes[0][2] // 2
+    worst = 0.0
+    for index in (0, -1):
+        a, b = workspace.a[index].float(), workspace.b[index].float()
+        ref = torch.nn.functional.silu(a @ b[:, :f]) * (a @ b[:, f:])
+        worst = max(worst, float((outputs[index].float() - ref).abs().max()) / float(ref.abs().max()))
+    for _ in range(warmup):
+        launch_gate_up_swiglu(workspace)
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(steps):
+        launch_gate_up_swiglu(workspace)
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    flops = sum(gemm_flops(*s) for s in workspace.shapes)
+    nbytes = sum(2 * (mm * k + k * n + mm * n // 2) for mm, k, n in workspace.shapes)
+    row = {
+        "case": f"dsv3_w1_ep_me{m}_swiglu", "experts": workspace.problem_count,
+        "shape_mkn": list(workspace.shapes[0]), "ms": ms, "tflops": flops / (ms * 1e9),
+        "gbs": nbytes / (ms * 1e6), "bound": "mfma", "frac": flops / (ms * 1e9) / PEAK_BF16_TFLOPS,
+        "config": workspace.swiglu_config.as_dict(), "scheduler": workspace.scheduler,
+        "epilogue": "silu(gate)*up fused, H [M_e, F] stored", "normwise_error_sampled": worst,
+        "correct": bool(worst <= 1e-2), "flops": flops, "ideal_bytes": nbytes,
+    }
+    del workspace
+    torch.cuda.empty_cache()
+    return row
+
+
 def _traffic_from_profiles(case: str):
     """HBM bytes per launch recorded by a committed rocprofv3 counter summary, if any."""
     path = REPO / "profiles" / f"{case}_hbm_traffic.md"
@@ -212,6 +258,7 @@ def main(argv=None) -> int:
         for projection, parallel_type, m in (("W1", "EP", 8), ("W1", "TP", 512), ("W1", "TP", 8),
                                             ("W2", "EP", 512), ("W2", "TP", 512), ("W2", "EP", 8)):
             cases.append(_case(projection, parallel_type, m, max(5, args.steps // 2), 2))
+        cases.append(_swiglu_case(512, max(5, args.steps // 2), 2))
     traffic = _traffic_from_profiles(headline["case"])
     tp = next((c for c in cases if c["case"] == "dsv3_w1_tp_me512"), None)
     line = {

@@ -77,6 +77,29 @@ int moegemm_grouped_gemm(const int64_t* a_ptrs, const int64_t* b_ptrs, const int
                          int32_t num_stages, int32_t grid_size, int32_t vector_layout, void* stream);
 
 /*
+ * Packed Gate+Up projection with the SwiGLU activation fused into the epilogue: for each problem e
+ * with B_e = [gate | up] of n = 2F columns (the packed W13 weights of reference
+ * kernels/grouped_gemm.py:575-594 build_fused_gate_up_workspace), H_e[m, j] =
+ * silu(sum_k A_e[m,k] B_e[k,j]) * sum_k A_e[m,k] B_e[k,F+j] for j < F, computed from the fp32
+ * accumulators and stored in the operand dtype into H_e [M_e, F] (h_ptrs; in generic mode the
+ * strides table's cm/cn are H's).  The reference keeps the activation outside its timed GEMM
+ * (README.md:55-57) and has no such kernel; this is the next step of the path, timed as a
+ * separate labelled variant.  Same tables, tile config and grid as moegemm_grouped_gemm; requires
+ * fp16/bf16, vector_layout != 0, F a multiple of 8 and a tile with moegemm_kernel_swiglu() == 1.
+ */
+int moegemm_grouped_gemm_swiglu(const int64_t* a_ptrs, const int64_t* b_ptrs, const int64_t* h_ptrs,
+                                const int32_t* dims, const int64_t* strides, int32_t problem_count,
+                                int32_t m, int32_t n, int32_t k, int32_t homogeneous,
+                                int32_t total_tiles, int32_t dtype, int32_t block_m,
+                                int32_t block_n, int32_t block_k, int32_t group_size_m,
+                                int32_t num_warps, int32_t num_stages, int32_t grid_size,
+                                int32_t vector_layout, void* stream);
+
+/* 1 when compiled kernel `index` of `dtype` can run the SwiGLU epilogue, 0 when not, < 0 on a bad
+ * index.  No counterpart in the reference (its Triton pools have no fused epilogue). */
+int moegemm_kernel_swiglu(int dtype, int index);
+
+/*
  * Grouped GEMM over the expert-sorted layout of torch.nn.functional.grouped_mm (2-D A, 3-D B):
  * for each group e, C[r0:r1, :] = A[r0:r1, :] @ B[e] with r0 = offs[e-1] (0 for e = 0) and
  * r1 = offs[e], fp32 accumulation.  A is [rows, k] (row stride stride_am), B is [group_count, k, n]

@@ -120,14 +120,30 @@ int moegemm_kernel_info(int dtype, int index, int32_t* out7) {
   return MOEGEMM_OK;
 }
 
-int moegemm_grouped_gemm(const int64_t* a_ptrs, const int64_t* b_ptrs, const int64_t* c_ptrs, const int32_t* dims,
-                         const int64_t* strides, int32_t problem_count, int32_t m, int32_t n, int32_t k,
-                         int32_t homogeneous, int32_t total_tiles, int32_t dtype, int32_t input_precision,
-                         int32_t block_m, int32_t block_n, int32_t block_k, int32_t group_size_m, int32_t num_warps,
-                         int32_t num_stages, int32_t grid_size, int32_t vector_layout, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int grouped_impl(const int64_t* a_ptrs, const int64_t* b_ptrs, const int64_t* c_ptrs, const int32_t* dims,
+                 const int64_t* strides, int32_t problem_count, int32_t m, int32_t n, int32_t k, int32_t homogeneous,
+                 int32_t total_tiles, int32_t dtype, int32_t input_precision, int32_t block_m, int32_t block_n,
+                 int32_t block_k, int32_t group_size_m, int32_t num_warps, int32_t num_stages, int32_t grid_size,
+                 int32_t vector_layout, bool swiglu, void* stream) {
   const KernelEntry* e = nullptr;
   int rc = check_common(dtype, input_precision, group_size_m, &e, block_m, block_n, block_k, num_warps, num_stages);
   if (rc != MOEGEMM_OK) return rc;
+  if (swiglu) {
+    if (dtype != DT_BF16 && dtype != DT_F16)
+      return fail(MOEGEMM_ERR_INVALID, "the SwiGLU epilogue needs fp16 or bf16 operands");
+    if (!vector_layout)
+      return fail(MOEGEMM_ERR_INVALID, "the SwiGLU epilogue needs the vector layout (LDS-DMA kernel)");
+    if (!e->swiglu_ok)
+      return fail(MOEGEMM_ERR_INVALID,
+                  "tile %dx%dx%d with %d waves cannot pair gate and up fragments (odd fragments per wave)",
+                  block_m, block_n, block_k, num_warps);
+    if (homogeneous && n % 16)
+      return fail(MOEGEMM_ERR_INVALID, "packed Gate+Up width must be a multiple of 16 (got %d)", n);
+  }
   if (problem_count <= 0) return fail(MOEGEMM_ERR_INVALID, "problem_count must be positive (got %d)", problem_count);
   if (!a_ptrs || !b_ptrs || !c_ptrs) return fail(MOEGEMM_ERR_INVALID, "pointer tables must be non-null");
   if (total_tiles < 0) return fail(MOEGEMM_ERR_INVALID, "total_tiles must be non-negative");
@@ -139,6 +155,7 @@ int moegemm_grouped_gemm(const int64_t* a_ptrs, const int64_t* b_ptrs, const int
   p.G = problem_count;
   p.group_m = group_size_m;
   p.tf32 = input_precision == MOEGEMM_PRECISION_TF32;
+  p.swiglu = swiglu ? 1 : 0;
   if (homogeneous) {
     if (m <= 0 || n <= 0 || k <= 0)
       return fail(MOEGEMM_ERR_INVALID, "homogeneous shape must be positive (m=%d n=%d k=%d)", m, n, k);
@@ -159,6 +176,39 @@ int moegemm_grouped_gemm(const int64_t* a_ptrs, const int64_t* b_ptrs, const int
   if (p.total_tiles == 0) return MOEGEMM_OK;
   int grid = grid_size <= 0 ? p.total_tiles : (grid_size < p.total_tiles ? grid_size : p.total_tiles);
   return launch(e, p, grid, vector_layout != 0, stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+int moegemm_grouped_gemm(const int64_t* a_ptrs, const int64_t* b_ptrs, const int64_t* c_ptrs, const int32_t* dims,
+                         const int64_t* strides, int32_t problem_count, int32_t m, int32_t n, int32_t k,
+                         int32_t homogeneous, int32_t total_tiles, int32_t dtype, int32_t input_precision,
+                         int32_t block_m, int32_t block_n, int32_t block_k, int32_t group_size_m, int32_t num_warps,
+                         int32_t num_stages, int32_t grid_size, int32_t vector_layout, void* stream) {
+  return grouped_impl(a_ptrs, b_ptrs, c_ptrs, dims, strides, problem_count, m, n, k, homogeneous, total_tiles, dtype,
+                      input_precision, block_m, block_n, block_k, group_size_m, num_warps, num_stages, grid_size,
+                      vector_layout, false, stream);
+}
+
+int moegemm_grouped_gemm_swiglu(const int64_t* a_ptrs, const int64_t* b_ptrs, const int64_t* h_ptrs,
+                                const int32_t* dims, const int64_t* strides, int32_t problem_count, int32_t m,
+                                int32_t n, int32_t k, int32_t homogeneous, int32_t total_tiles, int32_t dtype,
+                                int32_t block_m, int32_t block_n, int32_t block_k, int32_t group_size_m,
+                                int32_t num_warps, int32_t num_stages, int32_t grid_size, int32_t vector_layout,
+                                void* stream) {
+  return grouped_impl(a_ptrs, b_ptrs, h_ptrs, dims, strides, problem_count, m, n, k, homogeneous, total_tiles, dtype,
+                      MOEGEMM_PRECISION_IEEE, block_m, block_n, block_k, group_size_m, num_warps, num_stages,
+                      grid_size, vector_layout, true, stream);
+}
+
+int moegemm_kernel_swiglu(int dtype, int index) {
+  int count = 0;
+  const KernelEntry* t = table_for(dtype, &count);
+  if (!t || index < 0 || index >= count)
+    return fail(MOEGEMM_ERR_INVALID, "kernel index %d out of range for dtype %d", index, dtype);
+  return t[index].swiglu_ok;
 }
 
 int moegemm_grouped_mm_offs(const void* a, const void* b, void* c, const int32_t* offs, int32_t group_count,

@@ -20,6 +20,12 @@
 //    from moving across.  No other vector-memory loads are issued while copies are in flight.
 //  * Fragment reads for K step kk+1 are issued before the MFMAs of step kk (register double
 //    buffering) so the MFMA pipe does not wait on LDS latency inside a slice.
+//  * SwiGLU epilogue (packed W13, B = [gate | up] with n = 2F columns): a tile of output columns
+//    [n0/2, n0/2 + BN/2) loads, into the first half of every wave's WTN-column block, the gate
+//    columns and, into the second half, the matching up columns (F + the same offsets).  Fragment
+//    fn and fn + FN/2 of a lane then cover the same output columns, so the epilogue forms
+//    silu(gate) * up from the fp32 accumulators in registers and stores F-wide rows.  Needs an
+//    even FN and F a multiple of 8 (checked by the host).
 // Preconditions (checked by the host before choosing this variant): fp16/bf16, unit inner strides,
 // row pitches and the K, N extents multiples of 8 elements, every matrix < 2 GiB.
 #pragma once
@@ -92,6 +98,8 @@ struct FastTile {
   static constexpr int XMIN = IA / NW + IB / NW;  // issues per stage every wave makes
   static constexpr int RPA = 64 / CA;             // A rows per issue
   static constexpr int RPB = 64 / CB;             // B rows per issue
+  static constexpr int CPW = WTN / 8;             // B chunks per wave column block
+  static constexpr bool SWIGLU_OK = FN % 2 == 0;  // gate and up fragments pair up inside a wave
   static constexpr int PREFIX = 512;
   static constexpr int PREFIX_OFFSET = STAGES * STAGE_BYTES;
   static constexpr int LDS_BYTES = PREFIX_OFFSET + (PREFIX + 1) * 4 + NT * 4;
@@ -123,7 +131,10 @@ struct FastTile {
     d.k = pd.k;
     const int rows = min(BM, pd.m - m0);
     d.ra = make_rsrc(pd.a + (int64_t)m0 * lda_bytes, (uint32_t)rows * lda_bytes);
-    d.rb = make_rsrc(pd.b + (int64_t)n0 * 2, (uint32_t)pd.k * d.ldb_bytes - (uint32_t)n0 * 2u);
+    if (pd.swiglu)
+      d.rb = make_rsrc(pd.b, (uint32_t)pd.k * d.ldb_bytes);
+    else
+      d.rb = make_rsrc(pd.b + (int64_t)n0 * 2, (uint32_t)pd.k * d.ldb_bytes - (uint32_t)n0 * 2u);
     d.lds_wave = lds_address(smem) + (uint32_t)__builtin_amdgcn_readfirstlane(wave) * 1024u;
 #pragma unroll
     for (int q = 0; q < QA; ++q) {
@@ -140,7 +151,15 @@ struct FastTile {
       const int r = j * RPB + lane / CB;
       const int pc = lane % CB;
       const int c = pc ^ swz_b(r, CB);
-      d.b_off[q] = (n0 + c * 8 < pd.n) ? (uint32_t)r * d.ldb_bytes + (uint32_t)c * 16u : kOutOfRange;
+      if (pd.swiglu) {
+        // Logical chunk c of the tile: wave block c / CPW; its first half gate, second half up.
+        const int f = pd.n >> 1, half = CPW / 2, cc = c % CPW;
+        const int ocol = (n0 >> 1) + (c / CPW) * (WTN / 2) + (cc % half) * 8;
+        const int gcol = cc < half ? ocol : f + ocol;
+        d.b_off[q] = ocol < f ? (uint32_t)r * d.ldb_bytes + (uint32_t)gcol * 2u : kOutOfRange;
+      } else {
+        d.b_off[q] = (n0 + c * 8 < pd.n) ? (uint32_t)r * d.ldb_bytes + (uint32_t)c * 16u : kOutOfRange;
+      }
     }
   }
 
@@ -260,9 +279,39 @@ struct FastTile {
     }
   }
 
+  __device__ static __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+
   __device__ static __forceinline__ void store_tile(const acc_t (&acc)[FM][FN], const ProblemDesc& pd, int m0,
                                                     int n0, int wave_m, int wave_n) {
     const int lane = threadIdx.x & 63;
+    if constexpr (SWIGLU_OK) {
+      if (pd.swiglu) {
+        const int f = pd.n >> 1;
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm) {
+          const int gm = m0 + wave_m * WTM + fm * MI + (lane % MI);
+          if (gm >= pd.m) continue;
+          char* crow = pd.c + (int64_t)gm * pd.scm * 2;
+#pragma unroll
+          for (int fn = 0; fn < FN / 2; ++fn) {
+#pragma unroll
+            for (int q = 0; q < ACC / 4; ++q) {
+              const int nloc = (MI == 32) ? (q * 8 + (lane >> 5) * 4) : ((lane >> 4) * 4);
+              const int gn = (n0 >> 1) + wave_n * (WTN / 2) + fn * MI + nloc;
+              if (gn < f) {
+                f32x4_t v;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] = silu(acc[fm][fn][q * 4 + i]) * acc[fm][fn + FN / 2][q * 4 + i];
+                store4<E>(crow + (int64_t)gn * 2, v);
+              }
+            }
+          }
+        }
+        return;
+      }
+    } else {
+      if (pd.swiglu) return;  // the host never selects this tile for the epilogue; store nothing
+    }
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
       const int gm = m0 + wave_m * WTM + fm * MI + (lane % MI);

@@ -69,6 +69,7 @@ struct KParams {
   int32_t total_tiles;
   int32_t group_m;
   int32_t tf32;          // fp32 only: round operands to TF32 (10-bit mantissa, ties away)
+  int32_t swiglu;        // packed Gate+Up epilogue: B = [gate | up] (n columns), output n/2 columns
 };
 
 struct ProblemDesc {
@@ -77,6 +78,7 @@ struct ProblemDesc {
   char* c;
   int32_t m, n, k;
   int64_t sam, sak, sbk, sbn, scm, scn;
+  int32_t swiglu;  // C holds silu(A @ B[:, :n/2]) * (A @ B[:, n/2:]), n/2 columns
 };
 
 // Wave-uniform copies: values derived from LDS (the generic-mode prefix search) are treated as
@@ -105,6 +107,7 @@ __device__ __forceinline__ void make_uniform(ProblemDesc& pd) {
   pd.sbn = uniform(pd.sbn);
   pd.scm = uniform(pd.scm);
   pd.scn = uniform(pd.scn);
+  pd.swiglu = uniform(pd.swiglu);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -410,6 +413,7 @@ struct GemmTile {
   __device__ static __forceinline__ void store_tile(const acc_t (&acc)[FM][FN], const ProblemDesc& pd, int m0,
                                                     int n0, int wave_m, int wave_n) {
     const int lane = threadIdx.x & 63;
+    if (pd.swiglu) return;  // the epilogue runs only in the LDS-DMA tiles; the host enforces it
     const bool vec_c = pd.scn == 1 && (pd.scm % 4) == 0 && (pd.n % 4) == 0 &&
                        ((reinterpret_cast<uintptr_t>(pd.c) & (4 * ES - 1)) == 0);
 #pragma unroll
@@ -574,7 +578,7 @@ __global__ void __launch_bounds__(T::NT) grouped_gemm_kernel(KParams p) {
       pd.b = reinterpret_cast<const char*>(p.b_ptrs[e]);
       pd.c = reinterpret_cast<char*>(p.c_ptrs[e]);
       pd.m = p.M; pd.n = p.N; pd.k = p.K;
-      pd.sam = p.K; pd.sak = 1; pd.sbk = p.N; pd.sbn = 1; pd.scm = p.N; pd.scn = 1;
+      pd.sam = p.K; pd.sak = 1; pd.sbk = p.N; pd.sbn = 1; pd.scm = p.swiglu ? p.N / 2 : p.N; pd.scn = 1;
     } else {
       // Advance prefix chunks until this tile falls inside the current one (t is block-uniform).
       while (t >= s_pref[T::PREFIX] && chunk_first + T::PREFIX < p.G) {
@@ -611,6 +615,7 @@ __global__ void __launch_bounds__(T::NT) grouped_gemm_kernel(KParams p) {
       const int mt = (pd.m + T::BM - 1) / T::BM, nt = (pd.n + T::BN - 1) / T::BN;
       group_m_order(local, mt, nt, p.group_m, tm, tn);
     }
+    pd.swiglu = p.swiglu;
     make_uniform(pd);
     T::run_tile(pd, uniform(tm), uniform(tn), smem, p.tf32 != 0);
   }

@@ -19,6 +19,7 @@ struct KernelEntry {
   int num_stages;  // LDS stages of the fast path's K pipeline
   int waves_m, waves_n;
   int lds_bytes;   // fast path if present, else general
+  int swiglu_ok;   // the fast path can run the packed Gate+Up SwiGLU epilogue (even FN)
   LaunchFn launch_fast;     // null when the dtype has no fast path
   LaunchFn launch_general;
 };
@@ -49,6 +50,7 @@ using FastTileT = typename FastTileFor<E, BM, BN, BK, WM, WN, S>::type;
 #define MOEGEMM_ENTRY16(E, BM, BN, BK, WM, WN, S)                                             \
   KernelEntry{E::dtype, BM, BN, BK, (WM) * (WN), S, WM, WN,                                   \
               MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S)::LDS_BYTES,                              \
+              MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S)::SWIGLU_OK ? 1 : 0,                      \
               &launch_tile<MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S)>,                          \
               &launch_tile<MOEGEMM_GEN(E, BM, BN, BK, WM, WN)>},
 
@@ -56,7 +58,7 @@ using FastTileT = typename FastTileFor<E, BM, BN, BK, WM, WN, S>::type;
   template __global__ void grouped_gemm_kernel<MOEGEMM_GEN(E, BM, BN, BK, WM, WN)>(KParams);
 #define MOEGEMM_ENTRY32(E, BM, BN, BK, WM, WN, S)                                             \
   KernelEntry{E::dtype, BM, BN, BK, (WM) * (WN), S, WM, WN,                                   \
-              MOEGEMM_GEN(E, BM, BN, BK, WM, WN)::LDS_BYTES, nullptr,                         \
+              MOEGEMM_GEN(E, BM, BN, BK, WM, WN)::LDS_BYTES, 0, nullptr,                      \
               &launch_tile<MOEGEMM_GEN(E, BM, BN, BK, WM, WN)>},
 
 // 16-bit menu (bf16 and f16 share it): large-M MFMA-bound tiles down to skinny-M streaming tiles.

@@ -5,6 +5,7 @@ from .grouped_gemm import (
     build_fused_gate_up_workspace,
     build_grouped_workspace,
     grouped_candidate_configs,
+    launch_gate_up_swiglu,
     launch_grouped,
 )
 from .grouped_mm import (
@@ -43,6 +44,7 @@ __all__ = [
     "grouped_mm",
     "last_grouped_mm_config",
     "last_matmul_config",
+    "launch_gate_up_swiglu",
     "launch_grouped",
     "launch_grouped_offsets",
     "launch_matmul",

@@ -44,6 +44,12 @@ SIGNATURES = {
         [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
          _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
     ),
+    "moegemm_grouped_gemm_swiglu": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
+    ),
+    "moegemm_kernel_swiglu": (ctypes.c_int, [ctypes.c_int, ctypes.c_int]),
     "moegemm_grouped_mm_offs": (
         ctypes.c_int,
         [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i32, _i32,
@@ -115,6 +121,20 @@ def compiled_kernels(dtype_code: int) -> tuple[tuple[int, int, int, int, int, in
         check(lib.moegemm_kernel_info(dtype_code, index, out))
         rows.append(tuple(int(v) for v in out))
     return tuple(rows)
+
+
+@lru_cache(maxsize=None)
+def swiglu_tiles(dtype_code: int) -> frozenset:
+    """Tile keys (block_m, block_n, block_k, num_warps, num_stages) that can run the SwiGLU epilogue."""
+    lib = library()
+    keys = set()
+    for index, row in enumerate(compiled_kernels(dtype_code)):
+        status = lib.moegemm_kernel_swiglu(dtype_code, index)
+        if status < 0:
+            check(status)
+        if status == 1:
+            keys.add(tuple(row[:5]))
+    return frozenset(keys)
 
 
 def dtype_code(dtype) -> int:

@@ -61,6 +61,11 @@ class GroupedWorkspace:
     homogeneous: bool
     operation: str = "gemm"
     scheduler: str = "not_launched"
+    # Fused SwiGLU outputs H_e [M_e, N_e / 2] and their tables (allocated by launch_gate_up_swiglu).
+    h: list | None = None
+    h_ptrs: object = None
+    h_strides: object = None
+    swiglu_config: KernelConfig | None = None
 
     @property
     def problem_count(self) -> int:
@@ -367,3 +372,104 @@ def launch_grouped(
     _launch_grouped_fixed(workspace, cfg, dtype_code, precision)
     workspace.config = cfg
     workspace.scheduler = scheduler
+
+
+# ---------------------------------------------------------------------------------------------
+# Packed Gate+Up with the SwiGLU activation fused into the epilogue (one launch).
+
+def _swiglu_problem_ok(a, b, h) -> bool:
+    m, k = a.shape
+    n = b.shape[1]
+    sam, sak = a.stride()
+    sbk, sbn = b.stride()
+    shm, shn = h.stride()
+    return (
+        sak == 1 and sbn == 1 and shn == 1 and n % 16 == 0 and tuple(h.shape) == (m, n // 2)
+        and k % 8 == 0 and sam % 8 == 0 and sbk % 8 == 0 and shm % 4 == 0
+        and sam >= k and sbk >= n and shm >= n // 2
+        and a.data_ptr() % 16 == 0 and b.data_ptr() % 16 == 0 and h.data_ptr() % 8 == 0
+        and m * sam * 2 < _TWO_GIB and k * sbk * 2 < _TWO_GIB
+    )
+
+
+def _swiglu_outputs(workspace: GroupedWorkspace):
+    import torch
+
+    if workspace.h is None:
+        device = workspace.a[0].device
+        workspace.h = [torch.empty((m, n // 2), device=device, dtype=workspace.a[0].dtype)
+                       for m, _, n in workspace.shapes]
+        workspace.h_ptrs = torch.tensor([t.data_ptr() for t in workspace.h], device=device, dtype=torch.int64)
+        rows = [(a.stride(0), a.stride(1), b.stride(0), b.stride(1), h.stride(0), h.stride(1))
+                for a, b, h in zip(workspace.a, workspace.b, workspace.h)]
+        workspace.h_strides = torch.tensor(rows, device=device, dtype=torch.int64)
+    return workspace.h
+
+
+def _launch_swiglu_fixed(workspace: GroupedWorkspace, cfg: KernelConfig, dtype_code: int) -> None:
+    m, k, n = workspace.shapes[0]
+    status = _native.library().moegemm_grouped_gemm_swiglu(
+        workspace.a_ptrs.data_ptr(), workspace.b_ptrs.data_ptr(), workspace.h_ptrs.data_ptr(),
+        workspace.dims.data_ptr(), workspace.h_strides.data_ptr(),
+        workspace.problem_count, m, n, k, 1 if workspace.homogeneous else 0,
+        workspace.tile_count_for(cfg), dtype_code,
+        cfg.block_m, cfg.block_n, cfg.block_k, cfg.group_size_m, cfg.num_warps, cfg.num_stages,
+        _grid_size(workspace, cfg), 1, _native.current_stream_handle(workspace.a[0].device),
+    )
+    _native.check(status)
+
+
+_SWIGLU_AUTOTUNE_CACHE: dict[tuple, KernelConfig] = {}
+
+
+def swiglu_candidate_configs(workspace: GroupedWorkspace) -> tuple[KernelConfig, ...]:
+    """Grouped candidates restricted to tiles whose waves pair gate and up fragments."""
+    dtype_code = _native.dtype_code(workspace.a[0].dtype)
+    allowed = _native.swiglu_tiles(dtype_code)
+    ranked = grouped_candidate_configs(workspace.max_m, workspace.max_n, workspace.max_k,
+                                       problem_count=max(workspace.problem_count, 2),
+                                       sm_count=workspace.sm_count, dtype=workspace.a[0].dtype)
+    kept = tuple(c for c in ranked if c.tile_key in allowed)
+    if kept:
+        return kept
+    pool = [c for c in config_pool(workspace.a[0].dtype) if c.tile_key in allowed and c.group_size_m == 8]
+    return tuple(pool[:6])
+
+
+def launch_gate_up_swiglu(
+    workspace: GroupedWorkspace,
+    config: KernelConfig | None = None,
+    *,
+    autotune: bool = True,
+) -> list:
+    """H_e = silu(A_e @ B_e[:, :F]) * (A_e @ B_e[:, F:]) for every problem, in one kernel launch.
+
+    ``workspace`` holds packed Gate+Up weights (``build_fused_gate_up_workspace``): B_e has
+    2F columns, [gate | up].  The outputs H_e [M_e, F] are allocated on the first call and kept
+    in ``workspace.h``; the activation is computed from the fp32 accumulators, so H differs from
+    silu applied to a rounded C by at most the output rounding.  fp16/bf16 operands in the vector
+    layout only (ValueError otherwise).  Autotuning follows ``launch_grouped``: the first call per
+    workload measures the candidates, later calls are a cache lookup plus one launch.
+    """
+    _require_runtime()
+    dtype_code = _check_workspace(workspace)
+    if dtype_code == _native.DTYPE_F32:
+        raise ValueError("the fused SwiGLU epilogue needs fp16 or bf16 operands")
+    outputs = _swiglu_outputs(workspace)
+    if not all(_swiglu_problem_ok(a, b, h) for a, b, h in zip(workspace.a, workspace.b, outputs)):
+        raise ValueError("the fused SwiGLU epilogue needs unit inner strides, 16-byte aligned rows, "
+                         "K a multiple of 8 and a packed width N = 2F with F a multiple of 8")
+    cfg = config or workspace.swiglu_config
+    if autotune:
+        key = ("swiglu", workspace.problem_count, workspace.max_m, workspace.max_n, workspace.max_k,
+               workspace.shape_signature, workspace.device_signature, workspace.sm_count, dtype_code)
+        cfg = _SWIGLU_AUTOTUNE_CACHE.get(key)
+        if cfg is None:
+            cfg = _tune(swiglu_candidate_configs(workspace), lambda c: _launch_swiglu_fixed(workspace, c, dtype_code))
+            _SWIGLU_AUTOTUNE_CACHE[key] = cfg
+    elif cfg is None:
+        cfg = swiglu_candidate_configs(workspace)[0]
+    _launch_swiglu_fixed(workspace, cfg, dtype_code)
+    workspace.swiglu_config = cfg
+    workspace.scheduler = "homogeneous_persistent" if workspace.homogeneous else "generic_persistent"
+    return outputs

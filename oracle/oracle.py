@@ -25,6 +25,10 @@ Functions and the reference code they restate:
                                     offs[e-1]:offs[e]; rows past offs[-1] are unspecified there and
                                     zero here); pinned against
                                     torch's CPU grouped_mm and a brute force in tests/test_oracle.py.
+  * ``swiglu_reference``            silu(A @ B[:, :F]) * (A @ B[:, F:]) over packed Gate+Up weights
+                                    (the step after benchmark_moe.py:258-266's W13 product,
+                                    README.md:55-57): exact sums, float64 activation, one rounding;
+                                    pinned against torch CPU float64 and a planted gate/up swap.
   * ``offsets_tile_bound``          the host's tile-count bound for that layout (each group adds at
                                     most one partial M tile); pinned by exhaustive small cases.
   * ``to_bf16_bits`` / ``to_f16_bits``  round-to-nearest-even casts; pinned against torch/numpy.
@@ -158,6 +162,23 @@ def w13_reference(a: np.ndarray, b: np.ndarray, dtype: str, **kwargs) -> np.ndar
     gate = gemm(a, np.ascontiguousarray(b[:, :half]), dtype, **kwargs)
     up = gemm(a, np.ascontiguousarray(b[:, half:]), dtype, **kwargs)
     return np.concatenate([gate, up], axis=1)
+
+
+def swiglu_reference(a: np.ndarray, b: np.ndarray, dtype: str) -> np.ndarray:
+    """H = silu(A @ B[:, :F]) * (A @ B[:, F:]) for packed B = [gate | up], rounded once to dtype."""
+    n = b.shape[1]
+    if n % 2:
+        raise ValueError("packed Gate+Up weights need an even width")
+    half = n // 2
+    _, gate = gemm(a, np.ascontiguousarray(b[:, :half]), dtype, return_sums=True)
+    _, up = gemm(a, np.ascontiguousarray(b[:, half:]), dtype, return_sums=True)
+    h = gate / (1.0 + np.exp(-gate)) * up
+    h32 = h.astype(np.float32)
+    if dtype == "bf16":
+        return to_bf16_bits(h32)
+    if dtype == "fp16":
+        return to_f16_bits(h32)
+    return h32
 
 
 def offsets_groups(offs, rows: int) -> list[tuple[int, int]]:

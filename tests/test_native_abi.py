@@ -129,3 +129,17 @@ def test_missing_library_is_a_runtime_error(monkeypatch, tmp_path):
         monkeypatch.delenv("MOEGEMM_LIBRARY")
         _native.library.cache_clear()
     assert isinstance(_native.library(), ctypes.CDLL)
+
+
+def test_swiglu_tiles_are_exactly_the_even_fragment_tiles():
+    """The C library's epilogue flag equals the fragment-pairing rule (even N fragments per wave)."""
+    for code in (_native.DTYPE_F16, _native.DTYPE_BF16):
+        expected = set()
+        for bm, bn, bk, warps, stages, _lds, waves_m in _native.compiled_kernels(code):
+            wtm, wtn = bm // waves_m, bn // (warps // waves_m)
+            mi = 32 if wtm >= 32 and wtn >= 32 else 16
+            if (wtn // mi) % 2 == 0:
+                expected.add((bm, bn, bk, warps, stages))
+        assert _native.swiglu_tiles(code) == frozenset(expected)
+    assert _native.swiglu_tiles(_native.DTYPE_F32) == frozenset()
+    assert _native.library().moegemm_kernel_swiglu(_native.DTYPE_BF16, 10_000) < 0

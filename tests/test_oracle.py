@@ -292,3 +292,27 @@ def test_offsets_tile_bound_covers_every_split(block_m, block_n):
                 ends = list(cuts) + [rows]
                 tiles = sum(math.ceil(m / block_m) for _, m in oracle.offsets_groups(ends, rows)) * math.ceil(n / block_n)
                 assert tiles <= bound
+
+
+# --------------------------------------------------------------------------------------------
+# Fused SwiGLU epilogue over packed Gate+Up weights
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_swiglu_reference_matches_torch_float64(dtype):
+    import torch
+
+    rng = np.random.default_rng(21)
+    m, k, f = 13, 40, 24
+    enc = {"bf16": oracle.to_bf16_bits, "fp16": oracle.to_f16_bits}[dtype]
+    a = enc(rng.standard_normal((m, k)).astype(np.float32))
+    b = enc(rng.standard_normal((k, 2 * f)).astype(np.float32) * 0.5)
+    ours = _values(oracle.swiglu_reference(a, b, dtype), dtype)
+    ta = torch.from_numpy(_values(a, dtype))
+    tb = torch.from_numpy(_values(b, dtype))
+    theirs = (torch.nn.functional.silu(ta @ tb[:, :f]) * (ta @ tb[:, f:])).numpy()
+    ulp = {"bf16": 2.0 ** -8, "fp16": 2.0 ** -11}[dtype]  # half an output ulp: one correct rounding
+    np.testing.assert_allclose(ours, theirs, rtol=ulp, atol=1e-30)
+    swapped = _values(oracle.swiglu_reference(a, np.concatenate([b[:, f:], b[:, :f]], axis=1), dtype), dtype)
+    assert not np.allclose(swapped, theirs, rtol=1e-2, atol=1e-3)  # planted: gate and up exchanged
+    with pytest.raises(ValueError):
+        oracle.swiglu_reference(a, b[:, :-1], dtype)
