@@ -95,6 +95,35 @@ int moegemm_grouped_gemm_swiglu(const int64_t* a_ptrs, const int64_t* b_ptrs, co
                                 int32_t num_warps, int32_t num_stages, int32_t grid_size,
                                 int32_t vector_layout, void* stream);
 
+/*
+ * Split-K in one launch, for problems with fewer output tiles than CUs (the reference's G = 1
+ * Mixtral EP path, kernels/grouped_gemm.py:629-640 -> kernels/matmul.py:373-433, runs one
+ * workgroup per tile and leaves most of the GPU idle on a skinny-N, long-K W2).  Each output tile
+ * is computed by `splits` units over K ranges of whole block_k slices; each unit writes its fp32
+ * partial tile into `workspace`, and the last unit of a tile (counted with one atomic per unit)
+ * sums the partials in split order (deterministic), casts and stores C, and re-arms the counter.
+ * `workspace` (256-byte aligned, at least moegemm_splitk_workspace_bytes() bytes) holds int32
+ * counters then fp32 partials; its counters must be zero before the first call and every call
+ * leaves them zero, so a captured graph can be replayed without clearing it.  Calls that share a
+ * workspace must not overlap (use one workspace per stream).  fp16/bf16 in the vector layout only
+ * (the LDS-DMA kernels); `splits` is clamped to the number of non-empty K ranges.
+ */
+int moegemm_splitk_workspace_bytes(int32_t tiles, int32_t splits, int32_t block_m, int32_t block_n,
+                                   int64_t* bytes);
+int moegemm_matmul_splitk(const void* a, const void* b, void* c, int32_t m, int32_t n, int32_t k,
+                          int64_t stride_am, int64_t stride_ak, int64_t stride_bk,
+                          int64_t stride_bn, int64_t stride_cm, int64_t stride_cn, int32_t dtype,
+                          int32_t block_m, int32_t block_n, int32_t block_k, int32_t group_size_m,
+                          int32_t num_warps, int32_t num_stages, int32_t splits, int32_t grid_size,
+                          void* workspace, int64_t workspace_bytes, void* stream);
+/* Homogeneous grouped counterpart (equal contiguous problems, vector_layout must be 1). */
+int moegemm_grouped_gemm_splitk(const int64_t* a_ptrs, const int64_t* b_ptrs, const int64_t* c_ptrs,
+                                int32_t problem_count, int32_t m, int32_t n, int32_t k,
+                                int32_t dtype, int32_t block_m, int32_t block_n, int32_t block_k,
+                                int32_t group_size_m, int32_t num_warps, int32_t num_stages,
+                                int32_t splits, int32_t grid_size, int32_t vector_layout,
+                                void* workspace, int64_t workspace_bytes, void* stream);
+
 /* 1 when compiled kernel `index` of `dtype` can run the SwiGLU epilogue, 0 when not, < 0 on a bad
  * index.  No counterpart in the reference (its Triton pools have no fused epilogue). */
 int moegemm_kernel_swiglu(int dtype, int index);

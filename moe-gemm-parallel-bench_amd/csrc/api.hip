@@ -77,6 +77,36 @@ int launch(const KernelEntry* e, KParams& p, int grid, bool vector_layout, void*
   return MOEGEMM_OK;
 }
 
+// Split-K workspace: int32 counters [tiles] (256-byte padded), then fp32 partials
+// [tiles][splits][block_m * block_n].
+int64_t splitk_bytes(int64_t tiles, int64_t splits, int64_t block_m, int64_t block_n) {
+  const int64_t counters = (tiles * 4 + 255) / 256 * 256;
+  return counters + tiles * splits * block_m * block_n * 4;
+}
+
+int setup_splits(KParams& p, int64_t tiles, int32_t k, int32_t splits, int32_t block_m, int32_t block_n,
+                 int32_t block_k, void* workspace, int64_t workspace_bytes) {
+  if (splits < 1 || splits > 64) return fail(MOEGEMM_ERR_INVALID, "splits must be in [1, 64] (got %d)", splits);
+  // Every split covers whole K slices; the effective count drops trailing empty splits.
+  const int64_t chunk = cdiv(cdiv(k, splits), block_k) * block_k;
+  const int64_t effective = cdiv(k, chunk);
+  if (tiles * effective > INT32_MAX) return fail(MOEGEMM_ERR_INVALID, "split-K unit count exceeds int32");
+  if (effective > 1) {
+    const int64_t need = splitk_bytes(tiles, effective, block_m, block_n);
+    if (!workspace || workspace_bytes < need)
+      return fail(MOEGEMM_ERR_INVALID, "split-K workspace of %lld bytes is smaller than the %lld needed",
+                  (long long)workspace_bytes, (long long)need);
+    if (reinterpret_cast<uintptr_t>(workspace) & 255)
+      return fail(MOEGEMM_ERR_INVALID, "split-K workspace must be 256-byte aligned");
+    p.counters = static_cast<int32_t*>(workspace);
+    p.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + (tiles * 4 + 255) / 256 * 256);
+  }
+  p.splits = (int32_t)effective;
+  p.k_chunk = (int32_t)chunk;
+  p.total_tiles = (int32_t)tiles;
+  return MOEGEMM_OK;
+}
+
 // Preconditions of the LDS-DMA fast path for one problem (see gemm_fast.h).
 bool vector_layout_ok(const void* a, const void* b, const void* c, int64_t m, int64_t n, int64_t k, int64_t sam,
                       int64_t sak, int64_t sbk, int64_t sbn, int64_t scm, int64_t scn, int dtype) {
@@ -201,6 +231,86 @@ int moegemm_grouped_gemm_swiglu(const int64_t* a_ptrs, const int64_t* b_ptrs, co
   return grouped_impl(a_ptrs, b_ptrs, h_ptrs, dims, strides, problem_count, m, n, k, homogeneous, total_tiles, dtype,
                       MOEGEMM_PRECISION_IEEE, block_m, block_n, block_k, group_size_m, num_warps, num_stages,
                       grid_size, vector_layout, true, stream);
+}
+
+int moegemm_splitk_workspace_bytes(int32_t tiles, int32_t splits, int32_t block_m, int32_t block_n, int64_t* bytes) {
+  if (tiles < 0 || splits < 1 || block_m <= 0 || block_n <= 0 || !bytes)
+    return fail(MOEGEMM_ERR_INVALID, "split-K workspace query needs tiles >= 0, splits >= 1 and a tile shape");
+  *bytes = splitk_bytes(tiles, splits, block_m, block_n);
+  return MOEGEMM_OK;
+}
+
+int moegemm_matmul_splitk(const void* a, const void* b, void* c, int32_t m, int32_t n, int32_t k, int64_t stride_am,
+                          int64_t stride_ak, int64_t stride_bk, int64_t stride_bn, int64_t stride_cm,
+                          int64_t stride_cn, int32_t dtype, int32_t block_m, int32_t block_n, int32_t block_k,
+                          int32_t group_size_m, int32_t num_warps, int32_t num_stages, int32_t splits,
+                          int32_t grid_size, void* workspace, int64_t workspace_bytes, void* stream) {
+  const KernelEntry* e = nullptr;
+  int rc = check_common(dtype, MOEGEMM_PRECISION_IEEE, group_size_m, &e, block_m, block_n, block_k, num_warps,
+                        num_stages);
+  if (rc != MOEGEMM_OK) return rc;
+  if (!a || !b || !c) return fail(MOEGEMM_ERR_INVALID, "matrix pointers must be non-null");
+  if (m <= 0 || n <= 0 || k <= 0) return fail(MOEGEMM_ERR_INVALID, "shape must be positive (m=%d n=%d k=%d)", m, n, k);
+  if (!vector_layout_ok(a, b, c, m, n, k, stride_am, stride_ak, stride_bk, stride_bn, stride_cm, stride_cn, dtype) ||
+      !e->launch_fast)
+    return fail(MOEGEMM_ERR_INVALID, "split-K needs fp16/bf16 operands in the vector layout");
+  const int64_t tiles = cdiv(m, block_m) * cdiv(n, block_n);
+  KParams p;
+  std::memset(&p, 0, sizeof(p));
+  p.mode = MODE_SINGLE;
+  p.a = a;
+  p.b = b;
+  p.c = c;
+  p.M = m;
+  p.N = n;
+  p.K = k;
+  p.sam = stride_am;
+  p.sak = stride_ak;
+  p.sbk = stride_bk;
+  p.sbn = stride_bn;
+  p.scm = stride_cm;
+  p.scn = stride_cn;
+  p.G = 1;
+  p.group_m = group_size_m;
+  rc = setup_splits(p, tiles, k, splits, block_m, block_n, block_k, workspace, workspace_bytes);
+  if (rc != MOEGEMM_OK) return rc;
+  const int64_t units = (int64_t)p.total_tiles * p.splits;
+  const int grid = grid_size <= 0 || grid_size > units ? (int)units : grid_size;
+  return launch(e, p, grid, true, stream);
+}
+
+int moegemm_grouped_gemm_splitk(const int64_t* a_ptrs, const int64_t* b_ptrs, const int64_t* c_ptrs,
+                                int32_t problem_count, int32_t m, int32_t n, int32_t k, int32_t dtype,
+                                int32_t block_m, int32_t block_n, int32_t block_k, int32_t group_size_m,
+                                int32_t num_warps, int32_t num_stages, int32_t splits, int32_t grid_size,
+                                int32_t vector_layout, void* workspace, int64_t workspace_bytes, void* stream) {
+  const KernelEntry* e = nullptr;
+  int rc = check_common(dtype, MOEGEMM_PRECISION_IEEE, group_size_m, &e, block_m, block_n, block_k, num_warps,
+                        num_stages);
+  if (rc != MOEGEMM_OK) return rc;
+  if (problem_count <= 0) return fail(MOEGEMM_ERR_INVALID, "problem_count must be positive (got %d)", problem_count);
+  if (!a_ptrs || !b_ptrs || !c_ptrs) return fail(MOEGEMM_ERR_INVALID, "pointer tables must be non-null");
+  if (m <= 0 || n <= 0 || k <= 0)
+    return fail(MOEGEMM_ERR_INVALID, "homogeneous shape must be positive (m=%d n=%d k=%d)", m, n, k);
+  if (!vector_layout || !e->launch_fast)
+    return fail(MOEGEMM_ERR_INVALID, "split-K needs fp16/bf16 operands in the vector layout");
+  const int64_t tiles = (int64_t)problem_count * cdiv(m, block_m) * cdiv(n, block_n);
+  KParams p;
+  std::memset(&p, 0, sizeof(p));
+  p.mode = MODE_HOMOGENEOUS;
+  p.a_ptrs = a_ptrs;
+  p.b_ptrs = b_ptrs;
+  p.c_ptrs = c_ptrs;
+  p.G = problem_count;
+  p.M = m;
+  p.N = n;
+  p.K = k;
+  p.group_m = group_size_m;
+  rc = setup_splits(p, tiles, k, splits, block_m, block_n, block_k, workspace, workspace_bytes);
+  if (rc != MOEGEMM_OK) return rc;
+  const int64_t units = (int64_t)p.total_tiles * p.splits;
+  const int grid = grid_size <= 0 || grid_size > units ? (int)units : grid_size;
+  return launch(e, p, grid, true, stream);
 }
 
 int moegemm_kernel_swiglu(int dtype, int index) {

@@ -26,6 +26,12 @@
 //    fn and fn + FN/2 of a lane then cover the same output columns, so the epilogue forms
 //    silu(gate) * up from the fp32 accumulators in registers and stores F-wide rows.  Needs an
 //    even FN and F a multiple of 8 (checked by the host).
+//  * Split-K units (KParams::splits > 1) end with split_store instead of the C store: the fp32
+//    partial tile goes to the caller's workspace, a device-scope release fence orders it before
+//    one atomic increment of the tile's counter, and the unit that brings the counter to `splits`
+//    re-arms it (writes 0), fences (device-scope acquire; the other units skip it, so a tile
+//    costs one cache invalidation) and sums all partials of the tile in split order —
+//    the same order whichever unit is last, so results are deterministic — then casts and stores C.
 // Preconditions (checked by the host before choosing this variant): fp16/bf16, unit inner strides,
 // row pitches and the K, N extents multiples of 8 elements, every matrix < 2 GiB.
 #pragma once
@@ -281,9 +287,63 @@ struct FastTile {
 
   __device__ static __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
 
+  __device__ static __forceinline__ void split_store(const acc_t (&acc)[FM][FN], const ProblemDesc& pd, int m0,
+                                                     int n0, int wave_m, int wave_n) {
+    __shared__ int s_last;
+    const int lane = threadIdx.x & 63;
+    float* tile_base = pd.partials + (int64_t)pd.tile * pd.splits * (BM * BN);
+    float* mine = tile_base + (int64_t)pd.split * (BM * BN);
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      const int rl = wave_m * WTM + fm * MI + (lane % MI);
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int q = 0; q < ACC / 4; ++q) {
+          const int cl = wave_n * WTN + fn * MI + ((MI == 32) ? (q * 8 + (lane >> 5) * 4) : ((lane >> 4) * 4));
+          const f32x4_t v = {acc[fm][fn][q * 4 + 0], acc[fm][fn][q * 4 + 1], acc[fm][fn][q * 4 + 2],
+                             acc[fm][fn][q * 4 + 3]};
+          *MOEGEMM_GLOBAL(f32x4_t, mine + rl * BN + cl) = v;
+        }
+    }
+    // Release (device scope): this unit's partial is written back before the counter moves.  Only
+    // the last unit acquires, so only one cache invalidation per tile.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const int last = atomicAdd(pd.counters + pd.tile, 1) == pd.splits - 1;
+      if (last) atomicExch(pd.counters + pd.tile, 0);
+      s_last = last;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      const int rl = wave_m * WTM + fm * MI + (lane % MI);
+      const int gm = m0 + rl;
+      if (gm >= pd.m) continue;
+      char* crow = pd.c + (int64_t)gm * pd.scm * 2;
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int q = 0; q < ACC / 4; ++q) {
+          const int cl = wave_n * WTN + fn * MI + ((MI == 32) ? (q * 8 + (lane >> 5) * 4) : ((lane >> 4) * 4));
+          if (n0 + cl >= pd.n) continue;
+          f32x4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
+          for (int sp = 0; sp < pd.splits; ++sp) sum += *MOEGEMM_GLOBAL(const f32x4_t, tile_base + sp * (BM * BN) + rl * BN + cl);
+          store4<E>(crow + (int64_t)(n0 + cl) * 2, sum);
+        }
+    }
+  }
+
   __device__ static __forceinline__ void store_tile(const acc_t (&acc)[FM][FN], const ProblemDesc& pd, int m0,
                                                     int n0, int wave_m, int wave_n) {
     const int lane = threadIdx.x & 63;
+    if (pd.splits > 1) {
+      split_store(acc, pd, m0, n0, wave_m, wave_n);
+      return;
+    }
     if constexpr (SWIGLU_OK) {
       if (pd.swiglu) {
         const int f = pd.n >> 1;

@@ -70,6 +70,14 @@ struct KParams {
   int32_t group_m;
   int32_t tf32;          // fp32 only: round operands to TF32 (10-bit mantissa, ties away)
   int32_t swiglu;        // packed Gate+Up epilogue: B = [gate | up] (n columns), output n/2 columns
+  // Split-K (single and homogeneous modes, LDS-DMA tiles): each output tile is computed by
+  // `splits` units over K ranges of k_chunk elements; units write fp32 partial tiles to
+  // `partials` ([tiles][splits][BM*BN]) and count arrivals in `counters` ([tiles], zero between
+  // launches); the last unit of a tile sums the partials in split order and stores C.
+  int32_t splits;
+  int32_t k_chunk;
+  float* partials;
+  int32_t* counters;
 };
 
 struct ProblemDesc {
@@ -79,6 +87,11 @@ struct ProblemDesc {
   int32_t m, n, k;
   int64_t sam, sak, sbk, sbn, scm, scn;
   int32_t swiglu;  // C holds silu(A @ B[:, :n/2]) * (A @ B[:, n/2:]), n/2 columns
+  int32_t splits;  // > 1: this unit covers one K range of output tile `tile`
+  int32_t split;
+  int32_t tile;
+  float* partials;
+  int32_t* counters;
 };
 
 // Wave-uniform copies: values derived from LDS (the generic-mode prefix search) are treated as
@@ -108,6 +121,11 @@ __device__ __forceinline__ void make_uniform(ProblemDesc& pd) {
   pd.scm = uniform(pd.scm);
   pd.scn = uniform(pd.scn);
   pd.swiglu = uniform(pd.swiglu);
+  pd.splits = uniform(pd.splits);
+  pd.split = uniform(pd.split);
+  pd.tile = uniform(pd.tile);
+  pd.partials = uniform(pd.partials);
+  pd.counters = uniform(pd.counters);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -413,7 +431,8 @@ struct GemmTile {
   __device__ static __forceinline__ void store_tile(const acc_t (&acc)[FM][FN], const ProblemDesc& pd, int m0,
                                                     int n0, int wave_m, int wave_n) {
     const int lane = threadIdx.x & 63;
-    if (pd.swiglu) return;  // the epilogue runs only in the LDS-DMA tiles; the host enforces it
+    // The SwiGLU and split-K epilogues run only in the LDS-DMA tiles (the host enforces it).
+    if (pd.swiglu || pd.splits > 1) return;
     const bool vec_c = pd.scn == 1 && (pd.scm % 4) == 0 && (pd.n % 4) == 0 &&
                        ((reinterpret_cast<uintptr_t>(pd.c) & (4 * ES - 1)) == 0);
 #pragma unroll
@@ -558,7 +577,11 @@ __global__ void __launch_bounds__(T::NT) grouped_gemm_kernel(KParams p) {
   const bool searched = p.mode == MODE_GENERIC || p.mode == MODE_OFFSETS;
   if (searched) load_prefix<T>(p, s_pref, s_tot, 0, 0);
 
-  for (int t = vid; t < p.total_tiles; t += grid) {
+  // Units: tile t, K split u / total_tiles (one split outside split-K launches).
+  const int splits = p.splits > 1 ? p.splits : 1;
+  const int units = p.total_tiles * splits;
+  for (int u = vid; u < units; u += grid) {
+    const int t = u % p.total_tiles;
     ProblemDesc pd;
     int tm, tn;
     if (p.mode == MODE_SINGLE) {
@@ -616,6 +639,17 @@ __global__ void __launch_bounds__(T::NT) grouped_gemm_kernel(KParams p) {
       group_m_order(local, mt, nt, p.group_m, tm, tn);
     }
     pd.swiglu = p.swiglu;
+    pd.splits = splits;
+    pd.split = u / p.total_tiles;
+    pd.tile = t;
+    pd.partials = p.partials;
+    pd.counters = p.counters;
+    if (splits > 1) {  // this unit's K range: shift A's columns and B's rows, shorten K
+      const int k_begin = pd.split * p.k_chunk;
+      pd.a += (int64_t)k_begin * pd.sak * T::ES;
+      pd.b += (int64_t)k_begin * pd.sbk * T::ES;
+      pd.k = min(p.k_chunk, pd.k - k_begin);
+    }
     make_uniform(pd);
     T::run_tile(pd, uniform(tm), uniform(tn), smem, p.tf32 != 0);
   }

@@ -17,8 +17,9 @@
 // memory(k + 1) on, by both groups.  Slice k + 1 must be complete at barrier 2k + 2: group 0 waits
 // for its own copies at the end of compute(k), group 1 at the end of memory(k) (each wave has
 // S - 2 younger slices of copies in flight at that point), and the barrier publishes them.
-// Group 0 executes one extra barrier after its last compute phase (storing its outputs first)
-// so both groups pass the same number of barriers per tile.  Copies of slices past K read
+// Group 0 executes one extra barrier after its last compute phase (storing its outputs first,
+// except for split-K units, whose epilogue synchronises the workgroup and so runs after it) so
+// both groups pass the same number of barriers per tile.  Copies of slices past K read
 // zeros into buffers nobody reads; a wave's copies complete in issue order and every LDS slot is
 // always written by the same wave, so the next tile's prologue needs no drain.
 #pragma once
@@ -89,7 +90,11 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
       if (!second) wait_vmcnt<(STAGES - 2) * XMIN>();
       phase_barrier();
     }
-    if (!second) {
+    if (pd.splits > 1) {
+      // The split epilogue has workgroup barriers of its own: align the groups first.
+      if (!second) phase_barrier();
+      Base::store_tile(acc, pd, m0, n0, wave_m, wave_n);
+    } else if (!second) {
       Base::store_tile(acc, pd, m0, n0, wave_m, wave_n);
       phase_barrier();
     } else {

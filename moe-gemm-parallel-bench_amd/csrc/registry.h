@@ -42,24 +42,28 @@ struct FastTileFor {
 template <class E, int BM, int BN, int BK, int WM, int WN, int S>
 using FastTileT = typename FastTileFor<E, BM, BN, BK, WM, WN, S>::type;
 #define MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S) FastTileT<E, BM, BN, BK, WM, WN, S>
-#define MOEGEMM_GEN(E, BM, BN, BK, WM, WN) GemmTile<E, BM, BN, BK, WM, WN>
+// The general kernel has no stage count; the wrapper keeps one instantiation per menu entry even
+// when two entries differ only in the fast path's stages.
+template <class E, int BM, int BN, int BK, int WM, int WN, int S>
+struct GemmTileEntry : GemmTile<E, BM, BN, BK, WM, WN> {};
+#define MOEGEMM_GEN(E, BM, BN, BK, WM, WN, S) GemmTileEntry<E, BM, BN, BK, WM, WN, S>
 
 #define MOEGEMM_INST16(E, BM, BN, BK, WM, WN, S)                                              \
   template __global__ void grouped_gemm_kernel<MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S)>(KParams); \
-  template __global__ void grouped_gemm_kernel<MOEGEMM_GEN(E, BM, BN, BK, WM, WN)>(KParams);
+  template __global__ void grouped_gemm_kernel<MOEGEMM_GEN(E, BM, BN, BK, WM, WN, S)>(KParams);
 #define MOEGEMM_ENTRY16(E, BM, BN, BK, WM, WN, S)                                             \
   KernelEntry{E::dtype, BM, BN, BK, (WM) * (WN), S, WM, WN,                                   \
               MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S)::LDS_BYTES,                              \
               MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S)::SWIGLU_OK ? 1 : 0,                      \
               &launch_tile<MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S)>,                          \
-              &launch_tile<MOEGEMM_GEN(E, BM, BN, BK, WM, WN)>},
+              &launch_tile<MOEGEMM_GEN(E, BM, BN, BK, WM, WN, S)>},
 
 #define MOEGEMM_INST32(E, BM, BN, BK, WM, WN, S) \
-  template __global__ void grouped_gemm_kernel<MOEGEMM_GEN(E, BM, BN, BK, WM, WN)>(KParams);
+  template __global__ void grouped_gemm_kernel<MOEGEMM_GEN(E, BM, BN, BK, WM, WN, S)>(KParams);
 #define MOEGEMM_ENTRY32(E, BM, BN, BK, WM, WN, S)                                             \
   KernelEntry{E::dtype, BM, BN, BK, (WM) * (WN), S, WM, WN,                                   \
-              MOEGEMM_GEN(E, BM, BN, BK, WM, WN)::LDS_BYTES, 0, nullptr,                      \
-              &launch_tile<MOEGEMM_GEN(E, BM, BN, BK, WM, WN)>},
+              MOEGEMM_GEN(E, BM, BN, BK, WM, WN, S)::LDS_BYTES, 0, nullptr,                      \
+              &launch_tile<MOEGEMM_GEN(E, BM, BN, BK, WM, WN, S)>},
 
 // 16-bit menu (bf16 and f16 share it): large-M MFMA-bound tiles down to skinny-M streaming tiles.
 // STAGES is sized to the 160 KiB LDS of a CU.
@@ -71,7 +75,7 @@ using FastTileT = typename FastTileFor<E, BM, BN, BK, WM, WN, S>::type;
   X(E, 64, 256, 64, 1, 4, 3) X(E, 64, 128, 64, 2, 2, 4) X(E, 64, 64, 64, 2, 2, 4)            \
   X(E, 32, 256, 64, 1, 4, 4) X(E, 32, 128, 64, 1, 4, 4) X(E, 32, 128, 128, 1, 4, 3)          \
   X(E, 16, 256, 64, 1, 4, 4) X(E, 16, 256, 128, 1, 4, 2) X(E, 16, 128, 128, 1, 4, 4)         \
-  X(E, 16, 64, 128, 1, 4, 4)
+  X(E, 16, 64, 128, 1, 4, 4) X(E, 16, 64, 128, 1, 4, 7)
 
 // fp32 menu (general kernel, v_mfma_f32_16x16x4_f32); STAGES is the register-staged double buffer.
 #define MOEGEMM_MENU_F32(X, E)                                                               \

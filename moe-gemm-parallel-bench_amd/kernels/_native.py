@@ -50,6 +50,17 @@ SIGNATURES = {
          _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
     ),
     "moegemm_kernel_swiglu": (ctypes.c_int, [ctypes.c_int, ctypes.c_int]),
+    "moegemm_splitk_workspace_bytes": (ctypes.c_int, [_i32, _i32, _i32, _i32, ctypes.POINTER(_i64)]),
+    "moegemm_matmul_splitk": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i32,
+         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _vp],
+    ),
+    "moegemm_grouped_gemm_splitk": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+         _i32, _i32, _i32, _vp, _i64, _vp],
+    ),
     "moegemm_grouped_mm_offs": (
         ctypes.c_int,
         [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i32, _i32,
@@ -135,6 +146,29 @@ def swiglu_tiles(dtype_code: int) -> frozenset:
         if status == 1:
             keys.add(tuple(row[:5]))
     return frozenset(keys)
+
+
+def splitk_workspace_bytes(tiles: int, splits: int, block_m: int, block_n: int) -> int:
+    out = _i64(0)
+    check(library().moegemm_splitk_workspace_bytes(tiles, splits, block_m, block_n, ctypes.byref(out)))
+    return int(out.value)
+
+
+# Split-K workspaces, one per (device, stream).  A workspace is never released once handed out, so
+# a captured graph that recorded its address stays valid; a larger need allocates a new one.
+_SPLITK_WORKSPACES: dict[tuple[int, int], list] = {}
+_SPLITK_MIN_BYTES = 32 << 20
+
+
+def splitk_workspace(device, stream_handle: int, nbytes: int):
+    """A zero-initialised uint8 device tensor of at least ``nbytes`` for this device and stream."""
+    import torch
+
+    key = (torch.device(device).index or 0, int(stream_handle))
+    held = _SPLITK_WORKSPACES.setdefault(key, [])
+    if not held or held[-1].numel() < nbytes:
+        held.append(torch.zeros(max(nbytes, _SPLITK_MIN_BYTES), dtype=torch.uint8, device=device))
+    return held[-1]
 
 
 def dtype_code(dtype) -> int:

@@ -23,6 +23,9 @@ from dataclasses import dataclass
 from . import _native
 from .matmul import (
     KernelConfig,
+    last_matmul_split,
+    splitk_count,
+    with_split_options,
     _is_f32,
     _require_runtime,
     _tune,
@@ -66,6 +69,7 @@ class GroupedWorkspace:
     h_ptrs: object = None
     h_strides: object = None
     swiglu_config: KernelConfig | None = None
+    split_k: int = 1  # K splits of the most recent launch (1 = no split-K)
 
     @property
     def problem_count(self) -> int:
@@ -320,7 +324,33 @@ def _check_workspace(workspace: GroupedWorkspace) -> int:
     return _native.dtype_code(a0.dtype)
 
 
-def _launch_grouped_fixed(workspace: GroupedWorkspace, cfg: KernelConfig, dtype_code: int, precision: int) -> None:
+def _grouped_splits(workspace: GroupedWorkspace, cfg: KernelConfig, dtype_code: int, split_k) -> int:
+    if not workspace.homogeneous or not _vector_layout(workspace, dtype_code):
+        return 1
+    if split_k is not None:
+        return split_k
+    return splitk_count(workspace.tile_count_for(cfg), workspace.max_k, cfg.block_k, workspace.sm_count)
+
+
+def _launch_grouped_fixed(workspace: GroupedWorkspace, cfg: KernelConfig, dtype_code: int, precision: int,
+                          split_k=None) -> int:
+    """One launch; returns the K splits used."""
+    splits = _grouped_splits(workspace, cfg, dtype_code, split_k)
+    if splits > 1:
+        m, k, n = workspace.shapes[0]
+        tiles = workspace.tile_count_for(cfg)
+        stream = _native.current_stream_handle(workspace.a[0].device)
+        scratch = _native.splitk_workspace(workspace.a[0].device, stream,
+                                           _native.splitk_workspace_bytes(tiles, splits, cfg.block_m, cfg.block_n))
+        status = _native.library().moegemm_grouped_gemm_splitk(
+            workspace.a_ptrs.data_ptr(), workspace.b_ptrs.data_ptr(), workspace.c_ptrs.data_ptr(),
+            workspace.problem_count, m, n, k, dtype_code,
+            cfg.block_m, cfg.block_n, cfg.block_k, cfg.group_size_m, cfg.num_warps, cfg.num_stages, splits,
+            max(1, min(tiles * splits, workspace.sm_count * cfg.cta_multiplier)), 1,
+            scratch.data_ptr(), scratch.numel(), stream,
+        )
+        _native.check(status)
+        return splits
     lib = _native.library()
     m, k, n = workspace.shapes[0]
     status = lib.moegemm_grouped_gemm(
@@ -333,6 +363,7 @@ def _launch_grouped_fixed(workspace: GroupedWorkspace, cfg: KernelConfig, dtype_
         _native.current_stream_handle(workspace.a[0].device),
     )
     _native.check(status)
+    return 1
 
 
 _GROUPED_AUTOTUNE_CACHE: dict[tuple, KernelConfig] = {}
@@ -344,14 +375,24 @@ def launch_grouped(
     config: KernelConfig | None = None,
     *,
     autotune: bool = True,
+    split_k: int | None = None,
 ) -> None:
-    """Launch the persistent grouped kernel (autotuned per workload key, or a fixed config)."""
+    """Launch the persistent grouped kernel (autotuned per workload key, or a fixed config).
+
+    ``split_k`` (keyword-only, not in the reference's signature) as for ``launch_matmul``: None
+    splits K inside the one launch when a homogeneous 16-bit group has too few tiles to fill the
+    CUs; 1 disables it; n forces n.  ``workspace.split_k`` records what ran.
+    """
     _require_runtime()
+    if split_k is not None and split_k < 1:
+        raise ValueError("split_k must be None or a positive integer")
     cfg = config or workspace.config
     if workspace.problem_count == 1:
-        launch_matmul(workspace.a[0], workspace.b[0], workspace.c[0], cfg, input_precision, autotune=autotune)
+        launch_matmul(workspace.a[0], workspace.b[0], workspace.c[0], cfg, input_precision, autotune=autotune,
+                      split_k=split_k)
         workspace.config = last_matmul_config(cfg) if autotune else cfg
         workspace.scheduler = "single_problem_matmul"
+        workspace.split_k = last_matmul_split()
         return
     dtype_code = _check_workspace(workspace)
     precision = _native.precision_code(input_precision, dtype_code)
@@ -360,16 +401,21 @@ def launch_grouped(
         key = (
             scheduler, workspace.problem_count, workspace.max_m, workspace.max_n, workspace.max_k,
             workspace.shape_signature, workspace.device_signature, workspace.sm_count, dtype_code, precision,
+            split_k,
         )
-        cfg = _GROUPED_AUTOTUNE_CACHE.get(key)
-        if cfg is None:
+        tuned = _GROUPED_AUTOTUNE_CACHE.get(key)
+        if tuned is None:
             candidates = grouped_candidate_configs(
                 workspace.max_m, workspace.max_n, workspace.max_k,
                 problem_count=workspace.problem_count, sm_count=workspace.sm_count, dtype=workspace.a[0].dtype,
             )
-            cfg = _tune(candidates, lambda c: _launch_grouped_fixed(workspace, c, dtype_code, precision))
-            _GROUPED_AUTOTUNE_CACHE[key] = cfg
-    _launch_grouped_fixed(workspace, cfg, dtype_code, precision)
+            splittable = workspace.homogeneous and _vector_layout(workspace, dtype_code)
+            options = with_split_options(candidates, workspace.tile_count_for, workspace.max_k, workspace.sm_count,
+                                         split_k, splittable)
+            tuned = _tune(options, lambda o: _launch_grouped_fixed(workspace, o[0], dtype_code, precision, o[1]))
+            _GROUPED_AUTOTUNE_CACHE[key] = tuned
+        cfg, split_k = tuned
+    workspace.split_k = _launch_grouped_fixed(workspace, cfg, dtype_code, precision, split_k)
     workspace.config = cfg
     workspace.scheduler = scheduler
 

@@ -52,7 +52,7 @@ _MENU_16BIT: tuple[tuple[int, int, int, int, int], ...] = (
     (64, 256, 64, 4, 3), (64, 128, 64, 4, 4), (64, 64, 64, 4, 4),
     (32, 256, 64, 4, 4), (32, 128, 64, 4, 4), (32, 128, 128, 4, 3),
     (16, 256, 64, 4, 4), (16, 256, 128, 4, 2), (16, 128, 128, 4, 4),
-    (16, 64, 128, 4, 4),
+    (16, 64, 128, 4, 4), (16, 64, 128, 4, 7),
 )
 _MENU_F32: tuple[tuple[int, int, int, int, int], ...] = (
     (128, 128, 32, 4, 2), (64, 64, 32, 4, 2), (32, 64, 32, 4, 2),
@@ -252,7 +252,86 @@ def _require_runtime() -> None:
         raise RuntimeError(str(exc)) from exc
 
 
-def _launch_fixed(a, b, c, m, n, k, cfg: KernelConfig, dtype_code: int, precision: int) -> None:
+_TWO_GIB = 1 << 31
+
+
+def _vector_ok(a, b, c) -> bool:
+    """Preconditions of the LDS-DMA kernels for one 16-bit problem (see include/moegemm.h)."""
+    import torch
+
+    if a.dtype not in (torch.float16, torch.bfloat16):
+        return False
+    m, k = a.shape
+    n = b.shape[1]
+    sam, sak = a.stride()
+    sbk, sbn = b.stride()
+    scm, scn = c.stride()
+    return (
+        sak == 1 and sbn == 1 and scn == 1
+        and k % 8 == 0 and n % 8 == 0 and sam % 8 == 0 and sbk % 8 == 0 and scm % 4 == 0
+        and sam >= k and sbk >= n and scm >= n
+        and a.data_ptr() % 16 == 0 and b.data_ptr() % 16 == 0 and c.data_ptr() % 8 == 0
+        and m * sam * 2 < _TWO_GIB and k * sbk * 2 < _TWO_GIB
+    )
+
+
+def splitk_count(tiles: int, k: int, block_k: int, sm_count: int) -> int:
+    """K splits for a launch with ``tiles`` output tiles: 1 unless the tiles leave over half the CUs
+    idle; otherwise enough splits to give every CU a unit, each at least 4 K slices, at most 16."""
+    if tiles <= 0 or 2 * tiles > sm_count:
+        return 1
+    splits = min(sm_count // tiles, k // (4 * block_k), 16)
+    return splits if splits >= 2 else 1
+
+
+def with_split_options(configs, tiles_of, k: int, sm_count: int, split_k, splittable: bool) -> list:
+    """(config, split) tuning candidates: each config unsplit and, where ``splitk_count`` would
+    split it, also split — so measurement, not the heuristic alone, decides.  An explicit
+    ``split_k`` pins the split of every candidate."""
+    out = []
+    for cfg in configs:
+        if split_k is not None:
+            out.append((cfg, split_k))
+            continue
+        out.append((cfg, 1))
+        splits = splitk_count(tiles_of(cfg), k, cfg.block_k, sm_count) if splittable else 1
+        if splits > 1:
+            out.append((cfg, splits))
+    return out
+
+
+_LAST_SPLIT: list[int] = [1]
+
+
+def last_matmul_split() -> int:
+    """K splits used by the most recent ``launch_matmul`` call (1 = no split-K)."""
+    return _LAST_SPLIT[0]
+
+
+def _launch_fixed_splitk(a, b, c, m, n, k, cfg: KernelConfig, dtype_code: int, splits: int) -> None:
+    tiles = -(-m // cfg.block_m) * -(-n // cfg.block_n)
+    nbytes = _native.splitk_workspace_bytes(tiles, splits, cfg.block_m, cfg.block_n)
+    stream = _native.current_stream_handle(a.device)
+    workspace = _native.splitk_workspace(a.device, stream, nbytes)
+    status = _native.library().moegemm_matmul_splitk(
+        a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k,
+        a.stride(0), a.stride(1), b.stride(0), b.stride(1), c.stride(0), c.stride(1), dtype_code,
+        cfg.block_m, cfg.block_n, cfg.block_k, cfg.group_size_m, cfg.num_warps, cfg.num_stages, splits,
+        0, workspace.data_ptr(), workspace.numel(), stream,
+    )
+    _native.check(status)
+
+
+def _launch_fixed(a, b, c, m, n, k, cfg: KernelConfig, dtype_code: int, precision: int, split_k=None) -> int:
+    """One launch; returns the K splits used (``split_k`` None = ``splitk_count``'s choice)."""
+    splits = 1
+    if _vector_ok(a, b, c):
+        tiles = -(-m // cfg.block_m) * -(-n // cfg.block_n)
+        splits = split_k if split_k is not None else splitk_count(tiles, k, cfg.block_k,
+                                                                  _device_signature(a.device) % 1000)
+    if splits > 1:
+        _launch_fixed_splitk(a, b, c, m, n, k, cfg, dtype_code, splits)
+        return splits
     lib = _native.library()
     status = lib.moegemm_matmul(
         a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k,
@@ -262,6 +341,7 @@ def _launch_fixed(a, b, c, m, n, k, cfg: KernelConfig, dtype_code: int, precisio
         0, _native.current_stream_handle(a.device),
     )
     _native.check(status)
+    return 1
 
 
 def launch_matmul(
@@ -272,30 +352,38 @@ def launch_matmul(
     input_precision: str = "ieee",
     *,
     autotune: bool = True,
+    split_k: int | None = None,
 ) -> None:
-    """Launch C = A @ B: autotuned per shape key, or with an explicit config when autotune is false."""
+    """Launch C = A @ B: autotuned per shape key, or with an explicit config when autotune is false.
+
+    ``split_k`` (keyword-only, not in the reference's signature): None lets ``splitk_count`` split
+    K when the output tiles leave most CUs idle (fp16/bf16 vector layouts, one launch with a
+    deterministic in-kernel reduction); 1 disables it; n > 1 forces n splits.
+    """
     m, n, k = _validate_matrices(a, b, c)
     _require_runtime()
     dtype_code = _native.dtype_code(a.dtype)
     precision = _native.precision_code(input_precision, dtype_code)
+    if split_k is not None and split_k < 1:
+        raise ValueError("split_k must be None or a positive integer")
     if not autotune:
         cfg = config or select_config(m, n, k, a.dtype)
-        _launch_fixed(a, b, c, m, n, k, cfg, dtype_code, precision)
+        _LAST_SPLIT[0] = _launch_fixed(a, b, c, m, n, k, cfg, dtype_code, precision, split_k)
         return
     key = (
         m, n, k, tuple(a.stride()), tuple(b.stride()), tuple(c.stride()), dtype_code, precision,
-        _device_signature(a.device),
+        _device_signature(a.device), split_k,
     )
     best = _AUTOTUNE_CACHE.get(key)
     if best is None:
-        best = _tune(
-            matmul_candidate_configs(m, n, k, dtype=a.dtype,
-                                     sm_count=_device_signature(a.device) % 1000),
-            lambda cfg: _launch_fixed(a, b, c, m, n, k, cfg, dtype_code, precision),
-        )
+        sm_count = _device_signature(a.device) % 1000
+        configs = matmul_candidate_configs(m, n, k, dtype=a.dtype, sm_count=sm_count)
+        best = _tune(with_split_options(configs, lambda cfg: -(-m // cfg.block_m) * -(-n // cfg.block_n), k,
+                                        sm_count, split_k, _vector_ok(a, b, c)),
+                     lambda cand: _launch_fixed(a, b, c, m, n, k, cand[0], dtype_code, precision, cand[1]))
         _AUTOTUNE_CACHE[key] = best
-    _LAST_AUTOTUNED[0] = best
-    _launch_fixed(a, b, c, m, n, k, best, dtype_code, precision)
+    _LAST_AUTOTUNED[0] = best[0]
+    _LAST_SPLIT[0] = _launch_fixed(a, b, c, m, n, k, best[0], dtype_code, precision, best[1])
 
 
 def _warm_clocks(launch, budget_ms: float = 100.0) -> None:
@@ -313,7 +401,7 @@ def _warm_clocks(launch, budget_ms: float = 100.0) -> None:
     torch.cuda.synchronize()
 
 
-def _tune(candidates, launch) -> KernelConfig:
+def _tune(candidates, launch):
     """Hot-time every candidate (graph replays, bounded) after a clock warm-up; re-time the best three."""
     candidates = list(candidates)
     measured = []
