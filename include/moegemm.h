@@ -102,10 +102,12 @@ int moegemm_grouped_gemm_swiglu(const int64_t* a_ptrs, const int64_t* b_ptrs, co
  * is computed by `splits` units over K ranges of whole block_k slices; each unit writes its fp32
  * partial tile into `workspace`, and the last unit of a tile (counted with one atomic per unit)
  * sums the partials in split order (deterministic), casts and stores C, and re-arms the counter.
- * `workspace` (256-byte aligned, at least moegemm_splitk_workspace_bytes() bytes) holds int32
- * counters then fp32 partials; its counters must be zero before the first call and every call
- * leaves them zero, so a captured graph can be replayed without clearing it.  Calls that share a
- * workspace must not overlap (use one workspace per stream).  fp16/bf16 in the vector layout only
+ * `workspace` (256-byte aligned, at least moegemm_splitk_workspace_bytes() bytes) holds a fixed
+ * 256 KiB area of int32 tile counters (at most 65536 output tiles) then the fp32 partials; the
+ * counter area must be zero before the first call and every call leaves it zero, whatever its
+ * tile count or shape, so one workspace serves calls of any shape in any order and a captured
+ * graph can be replayed without clearing it.  Calls that share a workspace must not overlap (use
+ * one workspace per stream).  fp16/bf16 in the vector layout only
  * (the LDS-DMA kernels); `splits` is clamped to the number of non-empty K ranges.
  */
 int moegemm_splitk_workspace_bytes(int32_t tiles, int32_t splits, int32_t block_m, int32_t block_n,

@@ -77,11 +77,16 @@ int launch(const KernelEntry* e, KParams& p, int grid, bool vector_layout, void*
   return MOEGEMM_OK;
 }
 
-// Split-K workspace: int32 counters [tiles] (256-byte padded), then fp32 partials
-// [tiles][splits][block_m * block_n].
+// Split-K workspace: a fixed-size area of int32 tile counters at offset 0, then the fp32 partials
+// [tiles][splits][BM*BN].  The counter area has the same size whatever the launch, so the partials
+// of one launch never overlap the counters of another launch that shares the workspace (a counter
+// left non-zero by a stray partial would never see its tile's last unit, and the tile would go
+// unstored); counters are only ever written as counters, and every launch leaves them zero.
+constexpr int64_t kSplitCounterBytes = 256 * 1024;
+constexpr int64_t kSplitMaxTiles = kSplitCounterBytes / 4;
+
 int64_t splitk_bytes(int64_t tiles, int64_t splits, int64_t block_m, int64_t block_n) {
-  const int64_t counters = (tiles * 4 + 255) / 256 * 256;
-  return counters + tiles * splits * block_m * block_n * 4;
+  return kSplitCounterBytes + tiles * splits * block_m * block_n * 4;
 }
 
 int setup_splits(KParams& p, int64_t tiles, int32_t k, int32_t splits, int32_t block_m, int32_t block_n,
@@ -92,6 +97,9 @@ int setup_splits(KParams& p, int64_t tiles, int32_t k, int32_t splits, int32_t b
   const int64_t effective = cdiv(k, chunk);
   if (tiles * effective > INT32_MAX) return fail(MOEGEMM_ERR_INVALID, "split-K unit count exceeds int32");
   if (effective > 1) {
+    if (tiles > kSplitMaxTiles)
+      return fail(MOEGEMM_ERR_INVALID, "split-K supports at most %lld output tiles (got %lld)",
+                  (long long)kSplitMaxTiles, (long long)tiles);
     const int64_t need = splitk_bytes(tiles, effective, block_m, block_n);
     if (!workspace || workspace_bytes < need)
       return fail(MOEGEMM_ERR_INVALID, "split-K workspace of %lld bytes is smaller than the %lld needed",
@@ -99,7 +107,7 @@ int setup_splits(KParams& p, int64_t tiles, int32_t k, int32_t splits, int32_t b
     if (reinterpret_cast<uintptr_t>(workspace) & 255)
       return fail(MOEGEMM_ERR_INVALID, "split-K workspace must be 256-byte aligned");
     p.counters = static_cast<int32_t*>(workspace);
-    p.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + (tiles * 4 + 255) / 256 * 256);
+    p.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + kSplitCounterBytes);
   }
   p.splits = (int32_t)effective;
   p.k_chunk = (int32_t)chunk;

@@ -1,6 +1,7 @@
 """GPU tests at the BASELINE configurations' full per-rank sizes, plus graph capture and timing.
 
-Full-size checks use properties that do not depend on size:
+Full-size checks use properties that do not depend on size (the exact-integer check runs on all 36
+MoE cases of BASELINE configs[1..3], the random check on a representative subset):
   * exact-integer known answers on every expert (A = 1, B_e = e + 1 => C_e = K (e + 1), exact in
     the fp32 accumulator and representable in bf16/fp16 for these K) - catches any wrong index,
     missing tile, duplicated tile or tail error anywhere in the group;
@@ -39,6 +40,15 @@ CASES = [
 ]
 
 
+# Every MoE case of BASELINE configs[1..3]: 3 models x {W1, W2} x {EP, TP} x their M_e sweep.
+_MODELS = (("dsv3", (8, 64, 512), 7168, 2048, 256, 8, torch.bfloat16),
+           ("mixtral", (16, 128, 1024), 4096, 14336, 8, 8, torch.bfloat16),
+           ("qwen3", (4, 32, 256), 2048, 768, 128, 4, torch.float16))
+ALL_CASES = [(f"{name}_{proj.lower()}_{par.lower()}_me{m}", proj, par, m, h, f, e, p, dtype)
+             for name, ms, h, f, e, p, dtype in _MODELS for proj in ("W1", "W2") for par in ("EP", "TP")
+             for m in ms]
+
+
 @pytest.fixture(autouse=True)
 def _gpu_only():
     if not torch.cuda.is_available():
@@ -54,7 +64,7 @@ def _workspace(projection, parallel, m, h, f, e, p, dtype, seed=1234):
     return builder(shapes, dtype, seed)
 
 
-@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+@pytest.mark.parametrize("case", ALL_CASES, ids=[c[0] for c in ALL_CASES])
 def test_full_size_exact_integer_every_expert(case):
     from kernels.grouped_gemm import launch_grouped
 

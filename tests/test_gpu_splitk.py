@@ -4,7 +4,9 @@ Known answers whose K chunks differ (A = 1, B[k, n] = ((k // 64) % 5 - 2) + n % 
 summed the wrong K range, a lost partial or a double-counted split changes the exact integer
 result; seeded random inputs against the oracle (normwise bf16 <= 1e-2); M, N and K tails; forced
 and heuristic split counts; grouped homogeneous split-K; and a captured graph replayed several
-times with eager work in between (the per-tile counters must re-arm themselves).
+times with eager work in between (the per-tile counters must re-arm themselves); and launches of
+different tile counts sharing one stream's workspace in an order where a counter layout sized per
+launch put one launch's partials on the next launch's counters.
 """
 
 from __future__ import annotations
@@ -141,3 +143,20 @@ def test_graph_replays_rearm_the_counters():
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(c.double().cpu(), exact)
+
+
+def test_launches_of_different_tile_counts_share_one_workspace():
+    from kernels.matmul import KernelConfig, launch_matmul
+
+    m, k, n = 128, 14336, 4096  # Mixtral-8x7B EP rank, W2 at M_e = 128
+    a, b, exact = _known(m, k, n, torch.bfloat16)
+    # 16 tiles, then 128, 128 and 512 tiles: each launch has more tile counters than the one before.
+    sequence = ((KernelConfig(128, 256, 64, 8, 8, 3, 1), 16), (KernelConfig(16, 256, 128, 8, 4, 2, 1), 2),
+                (KernelConfig(64, 64, 64, 8, 4, 4, 1), 4), (KernelConfig(16, 64, 128, 8, 4, 7, 1), 3),
+                (KernelConfig(128, 256, 64, 8, 8, 3, 1), 16), (KernelConfig(16, 64, 128, 8, 4, 7, 1), 8))
+    for cfg, splits in sequence:
+        print(f"splitk shared workspace tile={cfg.tile_key} splits={splits}", flush=True)
+        c = torch.full((m, n), float("nan"), device="cuda", dtype=torch.bfloat16)
+        launch_matmul(a, b, c, cfg, autotune=False, split_k=splits)
+        torch.cuda.synchronize()
+        assert torch.equal(c.double().cpu(), exact), f"tile {cfg.tile_key} splits {splits}"

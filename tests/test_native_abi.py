@@ -143,3 +143,22 @@ def test_swiglu_tiles_are_exactly_the_even_fragment_tiles():
         assert _native.swiglu_tiles(code) == frozenset(expected)
     assert _native.swiglu_tiles(_native.DTYPE_F32) == frozenset()
     assert _native.library().moegemm_kernel_swiglu(_native.DTYPE_BF16, 10_000) < 0
+
+
+def test_splitk_workspace_has_a_fixed_counter_area():
+    """Partials start at the same offset for every launch shape, so launches of different tile
+    counts sharing one workspace never write partials over each other's tile counters."""
+    sizes = {(tiles, splits, bm, bn): _native.splitk_workspace_bytes(tiles, splits, bm, bn)
+             for tiles in (0, 1, 16, 128, 512, 65536) for splits in (2, 16) for bm, bn in ((16, 64), (256, 256))}
+    offsets = {nbytes - tiles * splits * bm * bn * 4 for (tiles, splits, bm, bn), nbytes in sizes.items()}
+    assert len(offsets) == 1
+    (counter_bytes,) = offsets
+    assert counter_bytes >= 65536 * 4 and counter_bytes % 256 == 0
+
+
+def test_splitk_entry_rejects_more_tiles_than_counters_without_launching():
+    lib = _native.library()
+    m, n, k = 4096, 16448, 1024  # 256 x 257 tiles of 16 x 64: one more column than the counters hold
+    status = lib.moegemm_matmul_splitk(256, 256, 256, m, n, k, k, 1, n, 1, n, 1, _native.DTYPE_BF16,
+                                       16, 64, 128, 1, 4, 4, 2, 0, None, 0, None)
+    assert status == _native.ERR_INVALID and "output tiles" in _native.last_error()
