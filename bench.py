@@ -118,6 +118,7 @@ def _case(projection: str, parallel_type: str, m: int, steps: int, warmup: int, 
         "ms": ms, "wall_ms": wall_ms, "tflops": tflops, "gbs": gbs, "bound": bound,
         "frac": tflops / PEAK_BF16_TFLOPS if bound == "mfma" else gbs / PEAK_HBM_GBS,
         "config": workspace.config.as_dict(), "scheduler": workspace.scheduler,
+        "tile_schedule": workspace.tile_schedule, "split_k": workspace.split_k,
         "normwise_error_sampled": error, "correct": bool(error <= 1e-2),
         "flops": flops, "ideal_bytes": nbytes,
     }

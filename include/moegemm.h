@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define MOEGEMM_ABI_VERSION 3
+#define MOEGEMM_ABI_VERSION 4
 
 #define MOEGEMM_OK 0
 #define MOEGEMM_ERR_INVALID (-1)   /* bad shape, pointer, dtype or parameter (Python: ValueError) */
@@ -35,6 +35,9 @@ extern "C" {
 
 #define MOEGEMM_PRECISION_IEEE 0 /* operands used as given */
 #define MOEGEMM_PRECISION_TF32 1 /* fp32 operands rounded to a 10-bit mantissa (ties away) */
+
+/* Size of the tile queue of the work-stealing launches (int32 counters, 256-byte aligned). */
+#define MOEGEMM_QUEUE_BYTES 256
 
 /* ABI version of the loaded library (MOEGEMM_ABI_VERSION when header and library agree). */
 int moegemm_abi_version(void);
@@ -75,6 +78,27 @@ int moegemm_grouped_gemm(const int64_t* a_ptrs, const int64_t* b_ptrs, const int
                          int32_t dtype, int32_t input_precision, int32_t block_m, int32_t block_n,
                          int32_t block_k, int32_t group_size_m, int32_t num_warps,
                          int32_t num_stages, int32_t grid_size, int32_t vector_layout, void* stream);
+
+/*
+ * moegemm_grouped_gemm with a work-stealing tile scheduler instead of the static one: the
+ * "persistent tile scheduler over (expert, m-tile, n-tile)" of reference
+ * kernels/grouped_gemm.py:321-482, whose programs take the fixed tiles pid, pid + grid, ...
+ * (:346-353, :397, :481); here the tiles are drawn at run time.  When grid_size is a multiple of 8 each XCD owns a
+ * contiguous eighth of the tiles (its workgroups take them from an atomic ticket counter) and a
+ * workgroup whose XCD has none left steals from the other XCDs' counters; otherwise one counter
+ * serves all.  `queue` is MOEGEMM_QUEUE_BYTES of device memory, zero before the first call; every
+ * call leaves it zero, so it can be reused without clearing (and replayed in a captured graph).
+ * Calls sharing a queue must not overlap (use one per stream).  Results are identical to
+ * moegemm_grouped_gemm's (each tile is computed the same way by whichever workgroup takes it).
+ */
+int moegemm_grouped_gemm_stealing(const int64_t* a_ptrs, const int64_t* b_ptrs,
+                                  const int64_t* c_ptrs, const int32_t* dims,
+                                  const int64_t* strides, int32_t problem_count, int32_t m,
+                                  int32_t n, int32_t k, int32_t homogeneous, int32_t total_tiles,
+                                  int32_t dtype, int32_t input_precision, int32_t block_m,
+                                  int32_t block_n, int32_t block_k, int32_t group_size_m,
+                                  int32_t num_warps, int32_t num_stages, int32_t grid_size,
+                                  int32_t vector_layout, void* queue, void* stream);
 
 /*
  * Packed Gate+Up projection with the SwiGLU activation fused into the epilogue: for each problem e
@@ -152,6 +176,16 @@ int moegemm_grouped_mm_offs(const void* a, const void* b, void* c, const int32_t
                             int32_t block_m, int32_t block_n, int32_t block_k,
                             int32_t group_size_m, int32_t num_warps, int32_t num_stages,
                             int32_t grid_size, void* stream);
+/* The same launch with the work-stealing tile scheduler and queue of
+ * moegemm_grouped_gemm_stealing; ragged offsets give tiles of unequal cost (partial M tiles). */
+int moegemm_grouped_mm_offs_stealing(const void* a, const void* b, void* c, const int32_t* offs,
+                                     int32_t group_count, int32_t rows, int32_t n, int32_t k,
+                                     int64_t stride_am, int64_t stride_bg, int64_t stride_bk,
+                                     int64_t stride_cm, int32_t dtype, int32_t input_precision,
+                                     int32_t block_m, int32_t block_n, int32_t block_k,
+                                     int32_t group_size_m, int32_t num_warps,
+                                     int32_t num_stages, int32_t grid_size, void* queue,
+                                     void* stream);
 
 /*
  * Masked single GEMM with arbitrary strides, C = A @ B.  Replaces the Triton launch of

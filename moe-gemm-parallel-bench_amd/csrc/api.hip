@@ -162,11 +162,21 @@ int moegemm_kernel_info(int dtype, int index, int32_t* out7) {
 
 namespace {
 
+// Work-stealing queue: MOEGEMM_QUEUE_BYTES of int32 counters, zero before the first launch (each
+// launch leaves them zero).  Null keeps the static schedule.
+int set_queue(KParams& p, void* queue) {
+  if (queue && (reinterpret_cast<uintptr_t>(queue) & 255))
+    return fail(MOEGEMM_ERR_INVALID, "the tile queue must be 256-byte aligned");
+  static_assert((kQueues + 1) * 4 <= MOEGEMM_QUEUE_BYTES, "queue counters fit the documented size");
+  p.queue = static_cast<int32_t*>(queue);
+  return MOEGEMM_OK;
+}
+
 int grouped_impl(const int64_t* a_ptrs, const int64_t* b_ptrs, const int64_t* c_ptrs, const int32_t* dims,
                  const int64_t* strides, int32_t problem_count, int32_t m, int32_t n, int32_t k, int32_t homogeneous,
                  int32_t total_tiles, int32_t dtype, int32_t input_precision, int32_t block_m, int32_t block_n,
                  int32_t block_k, int32_t group_size_m, int32_t num_warps, int32_t num_stages, int32_t grid_size,
-                 int32_t vector_layout, bool swiglu, void* stream) {
+                 int32_t vector_layout, bool swiglu, void* queue, void* stream) {
   const KernelEntry* e = nullptr;
   int rc = check_common(dtype, input_precision, group_size_m, &e, block_m, block_n, block_k, num_warps, num_stages);
   if (rc != MOEGEMM_OK) return rc;
@@ -211,6 +221,8 @@ int grouped_impl(const int64_t* a_ptrs, const int64_t* b_ptrs, const int64_t* c_
     p.strides = strides;
     p.total_tiles = total_tiles;
   }
+  rc = set_queue(p, queue);
+  if (rc != MOEGEMM_OK) return rc;
   if (p.total_tiles == 0) return MOEGEMM_OK;
   int grid = grid_size <= 0 ? p.total_tiles : (grid_size < p.total_tiles ? grid_size : p.total_tiles);
   return launch(e, p, grid, vector_layout != 0, stream);
@@ -227,7 +239,19 @@ int moegemm_grouped_gemm(const int64_t* a_ptrs, const int64_t* b_ptrs, const int
                          int32_t num_stages, int32_t grid_size, int32_t vector_layout, void* stream) {
   return grouped_impl(a_ptrs, b_ptrs, c_ptrs, dims, strides, problem_count, m, n, k, homogeneous, total_tiles, dtype,
                       input_precision, block_m, block_n, block_k, group_size_m, num_warps, num_stages, grid_size,
-                      vector_layout, false, stream);
+                      vector_layout, false, nullptr, stream);
+}
+
+int moegemm_grouped_gemm_stealing(const int64_t* a_ptrs, const int64_t* b_ptrs, const int64_t* c_ptrs,
+                                  const int32_t* dims, const int64_t* strides, int32_t problem_count, int32_t m,
+                                  int32_t n, int32_t k, int32_t homogeneous, int32_t total_tiles, int32_t dtype,
+                                  int32_t input_precision, int32_t block_m, int32_t block_n, int32_t block_k,
+                                  int32_t group_size_m, int32_t num_warps, int32_t num_stages, int32_t grid_size,
+                                  int32_t vector_layout, void* queue, void* stream) {
+  if (!queue) return fail(MOEGEMM_ERR_INVALID, "the work-stealing launch needs a tile queue");
+  return grouped_impl(a_ptrs, b_ptrs, c_ptrs, dims, strides, problem_count, m, n, k, homogeneous, total_tiles, dtype,
+                      input_precision, block_m, block_n, block_k, group_size_m, num_warps, num_stages, grid_size,
+                      vector_layout, false, queue, stream);
 }
 
 int moegemm_grouped_gemm_swiglu(const int64_t* a_ptrs, const int64_t* b_ptrs, const int64_t* h_ptrs,
@@ -238,7 +262,7 @@ int moegemm_grouped_gemm_swiglu(const int64_t* a_ptrs, const int64_t* b_ptrs, co
                                 void* stream) {
   return grouped_impl(a_ptrs, b_ptrs, h_ptrs, dims, strides, problem_count, m, n, k, homogeneous, total_tiles, dtype,
                       MOEGEMM_PRECISION_IEEE, block_m, block_n, block_k, group_size_m, num_warps, num_stages,
-                      grid_size, vector_layout, true, stream);
+                      grid_size, vector_layout, true, nullptr, stream);
 }
 
 int moegemm_splitk_workspace_bytes(int32_t tiles, int32_t splits, int32_t block_m, int32_t block_n, int64_t* bytes) {
@@ -329,11 +353,11 @@ int moegemm_kernel_swiglu(int dtype, int index) {
   return t[index].swiglu_ok;
 }
 
-int moegemm_grouped_mm_offs(const void* a, const void* b, void* c, const int32_t* offs, int32_t group_count,
-                            int32_t rows, int32_t n, int32_t k, int64_t stride_am, int64_t stride_bg,
-                            int64_t stride_bk, int64_t stride_cm, int32_t dtype, int32_t input_precision,
-                            int32_t block_m, int32_t block_n, int32_t block_k, int32_t group_size_m,
-                            int32_t num_warps, int32_t num_stages, int32_t grid_size, void* stream) {
+static int offsets_impl(const void* a, const void* b, void* c, const int32_t* offs, int32_t group_count, int32_t rows,
+                        int32_t n, int32_t k, int64_t stride_am, int64_t stride_bg, int64_t stride_bk,
+                        int64_t stride_cm, int32_t dtype, int32_t input_precision, int32_t block_m, int32_t block_n,
+                        int32_t block_k, int32_t group_size_m, int32_t num_warps, int32_t num_stages,
+                        int32_t grid_size, void* queue, void* stream) {
   const KernelEntry* e = nullptr;
   int rc = check_common(dtype, input_precision, group_size_m, &e, block_m, block_n, block_k, num_warps, num_stages);
   if (rc != MOEGEMM_OK) return rc;
@@ -376,7 +400,31 @@ int moegemm_grouped_mm_offs(const void* a, const void* b, void* c, const int32_t
                    (reinterpret_cast<uintptr_t>(a) & 15) == 0 && (reinterpret_cast<uintptr_t>(b) & 15) == 0 &&
                    (reinterpret_cast<uintptr_t>(c) & 7) == 0 && (int64_t)block_m * stride_am * 2 < (int64_t(1) << 31) &&
                    (int64_t)k * stride_bk * 2 < (int64_t(1) << 31);
+  rc = set_queue(p, queue);
+  if (rc != MOEGEMM_OK) return rc;
   return launch(e, p, grid, vec, stream);
+}
+
+int moegemm_grouped_mm_offs(const void* a, const void* b, void* c, const int32_t* offs, int32_t group_count,
+                            int32_t rows, int32_t n, int32_t k, int64_t stride_am, int64_t stride_bg,
+                            int64_t stride_bk, int64_t stride_cm, int32_t dtype, int32_t input_precision,
+                            int32_t block_m, int32_t block_n, int32_t block_k, int32_t group_size_m,
+                            int32_t num_warps, int32_t num_stages, int32_t grid_size, void* stream) {
+  return offsets_impl(a, b, c, offs, group_count, rows, n, k, stride_am, stride_bg, stride_bk, stride_cm, dtype,
+                      input_precision, block_m, block_n, block_k, group_size_m, num_warps, num_stages, grid_size,
+                      nullptr, stream);
+}
+
+int moegemm_grouped_mm_offs_stealing(const void* a, const void* b, void* c, const int32_t* offs,
+                                     int32_t group_count, int32_t rows, int32_t n, int32_t k, int64_t stride_am,
+                                     int64_t stride_bg, int64_t stride_bk, int64_t stride_cm, int32_t dtype,
+                                     int32_t input_precision, int32_t block_m, int32_t block_n, int32_t block_k,
+                                     int32_t group_size_m, int32_t num_warps, int32_t num_stages,
+                                     int32_t grid_size, void* queue, void* stream) {
+  if (!queue) return fail(MOEGEMM_ERR_INVALID, "the work-stealing launch needs a tile queue");
+  return offsets_impl(a, b, c, offs, group_count, rows, n, k, stride_am, stride_bg, stride_bk, stride_cm, dtype,
+                      input_precision, block_m, block_n, block_k, group_size_m, num_warps, num_stages, grid_size,
+                      queue, stream);
 }
 
 int moegemm_matmul(const void* a, const void* b, void* c, int32_t m, int32_t n, int32_t k, int64_t stride_am,

@@ -393,7 +393,11 @@ struct FastTile {
     }
   }
 
-  __device__ static __forceinline__ void run_tile(const ProblemDesc& pd, int tm, int tn, char* smem, bool) {
+  // `before_store` runs once every copy has landed, before the epilogue barrier and the C stores
+  // (a global atomic issued there overlaps them instead of delaying the in-order copy waits).
+  template <class Hook>
+  __device__ static __forceinline__ void run_tile(const ProblemDesc& pd, int tm, int tn, char* smem, bool,
+                                                  Hook&& before_store) {
     static_assert(KK % 2 == 0, "fragment double buffer alternates by K step");
     constexpr int HALF = FM / 2 > 0 ? FM / 2 : 1;  // fragment rows issued before the mid-slice barrier
     constexpr int NDS = FM + 2 * FN;                 // LDS reads per K step
@@ -451,6 +455,7 @@ struct FastTile {
     // All copies (including the out-of-range tail slices) landed and every wave is done reading
     // LDS before the next tile's prologue refills it.
     wait_vmcnt<0>();
+    before_store();
     compiler_fence();
     __builtin_amdgcn_s_barrier();
     compiler_fence();

@@ -78,6 +78,9 @@ struct KParams {
   int32_t k_chunk;
   float* partials;
   int32_t* counters;
+  // Work-stealing schedule (null = static): kQueues ticket counters, then one exit count; zero
+  // between launches (the last workgroup of a launch re-arms them).
+  int32_t* queue;
 };
 
 struct ProblemDesc {
@@ -461,7 +464,11 @@ struct GemmTile {
   }
 
   // -------------------------------------------------------------------------------------------
-  __device__ static __forceinline__ void run_tile(const ProblemDesc& pd, int tm, int tn, char* smem, bool tf32) {
+  // `before_store` runs once the K loop is done, before the C stores (the work-stealing scheduler
+  // draws its next ticket there).
+  template <class Hook>
+  __device__ static __forceinline__ void run_tile(const ProblemDesc& pd, int tm, int tn, char* smem, bool tf32,
+                                                  Hook&& before_store) {
     const int wave = threadIdx.x >> 6;
     const int wave_m = wave / WN, wave_n = wave % WN;
     const int m0 = tm * BM, n0 = tn * BN;
@@ -495,6 +502,7 @@ struct GemmTile {
       if (more) store_stage(st, nxt, nxt + A_BYTES);
       __syncthreads();
     }
+    before_store();
     store_tile(acc, pd, m0, n0, wave_m, wave_n);
   }
 };
@@ -563,6 +571,65 @@ __device__ __forceinline__ void load_prefix(const KParams& p, int* s_pref, int* 
   __syncthreads();
 }
 
+// Work-stealing tile queues (KParams::queue).  When the grid is a multiple of 8, workgroup b runs
+// on XCD b % 8 (round-robin dispatch) and XCD x owns units [lo(x), lo(x + 1)) — a contiguous run,
+// so the tiles sharing an expert's B panel stay in one XCD's L2; otherwise one queue owns all
+// units.  The `per` workgroups of an XCD take their first units statically (lo(x) + b / 8) and
+// draw later ones from ticket counter queue[x] (ticket c is unit lo(x) + per + c).  The ticket for
+// the next unit is drawn after the current tile's K loop, before its C stores: vector memory
+// operations complete in issue order, so an atomic issued earlier would hold up the tile's copy
+// waits, while here its latency overlaps the epilogue.  When a queue is drained, wave 0 reads all
+// counters at once (one lane each) and moves to the queue with the most units left, so units left
+// on a slow XCD are taken by idle ones and a drained workgroup learns that every queue is empty in
+// one round trip.  Every workgroup counts itself out in queue[kQueues] after its last claim has
+// returned, and the last one re-arms all counters to zero for the next launch.
+constexpr int kQueues = 8;
+
+struct TileQueue {
+  int32_t* q;
+  int nx, per, units;
+  int cur;           // queue of the last claim (starts at this workgroup's XCD)
+  uint32_t drained;  // bit y: queue y has no units left (known to wave 0)
+
+  __device__ int lo(int y) const { return (int)((int64_t)y * units / nx); }
+
+  // Wave 0 only (every lane, uniform control flow).  Lane 0 holds `c`, a ticket already drawn from
+  // queue `cur`, or -1.  Returns the next unit, or -1 when every queue is drained.  Each round
+  // either claims a unit or marks at least one more queue drained, so it ends within nx + 1 rounds.
+  __device__ int claim(int c) {
+    const int lane = (int)(threadIdx.x & 63);
+    for (int round = 0; round <= kQueues; ++round) {
+      if (!((drained >> cur) & 1u)) {
+        int u = -1;
+        if (lane == 0) {
+          if (c < 0) c = atomicAdd(q + cur, 1);
+          u = lo(cur) + per + c;
+          if (u >= lo(cur + 1)) u = -1;
+        }
+        u = __builtin_amdgcn_readfirstlane(u);
+        c = -1;
+        if (u >= 0) return u;
+        drained |= 1u << cur;
+      }
+      int left = 0;
+      if (lane < nx && !((drained >> lane) & 1u))
+        left = lo(lane + 1) - lo(lane) - per - __hip_atomic_load(q + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      drained |= (uint32_t)__builtin_amdgcn_ballot_w64(lane < nx && left <= 0) & ((1u << nx) - 1u);
+      int best = -1, most = 0;
+      for (int y = 0; y < nx; ++y) {
+        const int l = __builtin_amdgcn_readlane(left, y);
+        if (l > most) {
+          most = l;
+          best = y;
+        }
+      }
+      if (best < 0) return -1;
+      cur = best;
+    }
+    return -1;
+  }
+};
+
 template <class T>
 __global__ void __launch_bounds__(T::NT) grouped_gemm_kernel(KParams p) {
   __shared__ __attribute__((aligned(16))) char smem[T::LDS_BYTES];
@@ -580,7 +647,32 @@ __global__ void __launch_bounds__(T::NT) grouped_gemm_kernel(KParams p) {
   // Units: tile t, K split u / total_tiles (one split outside split-K launches).
   const int splits = p.splits > 1 ? p.splits : 1;
   const int units = p.total_tiles * splits;
-  for (int u = vid; u < units; u += grid) {
+  const bool stealing = p.queue != nullptr;
+  __shared__ int s_next[2];  // unit broadcast, alternating slots so a slow reader never sees the next
+  int parity = 0;
+  TileQueue tq{};
+  int u = vid;
+  // Wave 0 claims the next unit (-1: none left) and the workgroup takes it from LDS.
+  auto next_unit = [&](int ticket) {
+    if (threadIdx.x < 64) {
+      const int claimed = tq.claim(ticket);
+      if (threadIdx.x == 0) s_next[parity] = claimed;
+    }
+    __syncthreads();
+    u = uniform(s_next[parity]);
+    parity ^= 1;
+  };
+  if (stealing) {
+    tq.q = p.queue;
+    tq.nx = (grid & 7) == 0 ? kQueues : 1;
+    tq.per = grid / tq.nx;
+    tq.units = units;
+    tq.cur = (int)blockIdx.x & (tq.nx - 1);
+    tq.drained = 0;
+    u = tq.lo(tq.cur) + (int)blockIdx.x / tq.nx;
+    if (u >= tq.lo(tq.cur + 1)) next_unit(-1);  // this XCD has fewer units than workgroups
+  }
+  while (stealing ? u >= 0 : u < units) {
     const int t = u % p.total_tiles;
     ProblemDesc pd;
     int tm, tn;
@@ -603,6 +695,12 @@ __global__ void __launch_bounds__(T::NT) grouped_gemm_kernel(KParams p) {
       pd.m = p.M; pd.n = p.N; pd.k = p.K;
       pd.sam = p.K; pd.sak = 1; pd.sbk = p.N; pd.sbn = 1; pd.scm = p.swiglu ? p.N / 2 : p.N; pd.scn = 1;
     } else {
+      // A stolen unit may precede the loaded prefix chunk: restart from the first chunk.
+      if (t < s_pref[0]) {
+        chunk_first = 0;
+        __syncthreads();
+        load_prefix<T>(p, s_pref, s_tot, 0, 0);
+      }
       // Advance prefix chunks until this tile falls inside the current one (t is block-uniform).
       while (t >= s_pref[T::PREFIX] && chunk_first + T::PREFIX < p.G) {
         const int base = s_pref[T::PREFIX];
@@ -610,7 +708,13 @@ __global__ void __launch_bounds__(T::NT) grouped_gemm_kernel(KParams p) {
         __syncthreads();
         load_prefix<T>(p, s_pref, s_tot, chunk_first, base);
       }
-      if (t >= s_pref[T::PREFIX]) break;  // device dims describe fewer tiles than the host count
+      if (t >= s_pref[T::PREFIX]) {  // device dims describe fewer tiles than the host count
+        if (!stealing) break;
+        // Later units of this queue lie past the count too: mark it drained and move on.
+        tq.drained |= 1u << tq.cur;
+        next_unit(-1);
+        continue;
+      }
       int lo = 0, hi = T::PREFIX;           // largest i with s_pref[i] <= t
       while (hi - lo > 1) {
         const int mid = (lo + hi) >> 1;
@@ -651,7 +755,18 @@ __global__ void __launch_bounds__(T::NT) grouped_gemm_kernel(KParams p) {
       pd.k = min(p.k_chunk, pd.k - k_begin);
     }
     make_uniform(pd);
-    T::run_tile(pd, uniform(tm), uniform(tn), smem, p.tf32 != 0);
+    int ticket = -1;  // the next unit's ticket: drawn before the C stores, resolved after the tile
+    T::run_tile(pd, uniform(tm), uniform(tn), smem, p.tf32 != 0, [&] {
+      if (stealing && threadIdx.x == 0 && !((tq.drained >> tq.cur) & 1u)) ticket = atomicAdd(tq.q + tq.cur, 1);
+    });
+    if (stealing)
+      next_unit(ticket);
+    else
+      u += grid;
+  }
+  if (stealing && threadIdx.x == 0 && atomicAdd(p.queue + kQueues, 1) == grid - 1) {
+    for (int y = 0; y < kQueues; ++y) atomicExch(p.queue + y, 0);
+    atomicExch(p.queue + kQueues, 0);
   }
 }
 

@@ -50,7 +50,9 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
   static_assert(Base::IA % NW == 0 && Base::IB % NW == 0, "every wave issues the same number of copies");
   static_assert(STAGES >= 3, "group 1 needs at least one phase between issuing and publishing a slice");
 
-  __device__ static __forceinline__ void run_tile(const ProblemDesc& pd, int tm, int tn, char* smem, bool) {
+  template <class Hook>
+  __device__ static __forceinline__ void run_tile(const ProblemDesc& pd, int tm, int tn, char* smem, bool,
+                                                  Hook&& before_store) {
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int wave_m = wave / WN, wave_n = wave % WN;
     const bool second = wave >= NW / 2;
@@ -90,6 +92,7 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
       if (!second) wait_vmcnt<(STAGES - 2) * XMIN>();
       phase_barrier();
     }
+    before_store();  // before the C stores, as in FastTile
     if (pd.splits > 1) {
       // The split epilogue has workgroup barriers of its own: align the groups first.
       if (!second) phase_barrier();

@@ -13,6 +13,7 @@ from .grouped_mm import (
     build_offsets_workspace,
     grouped_mm,
     last_grouped_mm_config,
+    last_grouped_mm_schedule,
     launch_grouped_offsets,
 )
 from .matmul import (
@@ -43,6 +44,7 @@ __all__ = [
     "grouped_candidate_configs",
     "grouped_mm",
     "last_grouped_mm_config",
+    "last_grouped_mm_schedule",
     "last_matmul_config",
     "launch_gate_up_swiglu",
     "launch_grouped",

@@ -15,7 +15,7 @@ from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().with_name("libmoegemm.so")
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 OK = 0
 ERR_INVALID = -1
 ERR_NO_KERNEL = -2
@@ -44,6 +44,11 @@ SIGNATURES = {
         [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
          _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
     ),
+    "moegemm_grouped_gemm_stealing": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp],
+    ),
     "moegemm_grouped_gemm_swiglu": (
         ctypes.c_int,
         [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
@@ -65,6 +70,11 @@ SIGNATURES = {
         ctypes.c_int,
         [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i32, _i32,
          _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
+    ),
+    "moegemm_grouped_mm_offs_stealing": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i32, _i32,
+         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp],
     ),
     "moegemm_matmul": (
         ctypes.c_int,
@@ -169,6 +179,25 @@ def splitk_workspace(device, stream_handle: int, nbytes: int):
     if not held or held[-1].numel() < nbytes:
         held.append(torch.zeros(max(nbytes, _SPLITK_MIN_BYTES), dtype=torch.uint8, device=device))
     return held[-1]
+
+
+# Work-stealing tile queues, one per (device, stream), zeroed once and never released (launches
+# leave them zero; a captured graph keeps a valid address).
+QUEUE_BYTES = 256
+TILE_SCHEDULES = ("static", "stealing")
+_TILE_QUEUES: dict[tuple[int, int], object] = {}
+
+
+def tile_queue(device, stream_handle: int):
+    """The zero-initialised MOEGEMM_QUEUE_BYTES device buffer for this device and stream."""
+    import torch
+
+    key = (torch.device(device).index or 0, int(stream_handle))
+    queue = _TILE_QUEUES.get(key)
+    if queue is None:
+        queue = torch.zeros(QUEUE_BYTES // 4, dtype=torch.int32, device=device)
+        _TILE_QUEUES[key] = queue
+    return queue
 
 
 def dtype_code(dtype) -> int:

@@ -70,6 +70,7 @@ class GroupedWorkspace:
     h_strides: object = None
     swiglu_config: KernelConfig | None = None
     split_k: int = 1  # K splits of the most recent launch (1 = no split-K)
+    tile_schedule: str = "static"  # "static" or "stealing" (work-stealing tile queues) of the last launch
 
     @property
     def problem_count(self) -> int:
@@ -332,10 +333,25 @@ def _grouped_splits(workspace: GroupedWorkspace, cfg: KernelConfig, dtype_code: 
     return splitk_count(workspace.tile_count_for(cfg), workspace.max_k, cfg.block_k, workspace.sm_count)
 
 
+def with_schedule_options(options, tile_schedule: str | None) -> list:
+    """(config, split, schedule) tuning candidates: unsplit options run under both schedules
+    unless ``tile_schedule`` pins one; split options stay static."""
+    out = []
+    for cfg, split in options:
+        if split == 1 and tile_schedule is None:
+            out += [(cfg, 1, "static"), (cfg, 1, "stealing")]
+        elif split == 1 or tile_schedule != "stealing":
+            out.append((cfg, split, tile_schedule or "static"))
+    return out
+
+
 def _launch_grouped_fixed(workspace: GroupedWorkspace, cfg: KernelConfig, dtype_code: int, precision: int,
-                          split_k=None) -> int:
-    """One launch; returns the K splits used."""
+                          split_k=None, schedule: str = "static") -> int:
+    """One launch; returns the K splits used.  ``schedule`` "stealing" draws the tiles from the
+    work-stealing queues (unsplit launches only)."""
     splits = _grouped_splits(workspace, cfg, dtype_code, split_k)
+    if schedule == "stealing" and splits > 1:
+        raise ValueError("the work-stealing schedule runs unsplit launches only (split_k must be 1)")
     if splits > 1:
         m, k, n = workspace.shapes[0]
         tiles = workspace.tile_count_for(cfg)
@@ -353,20 +369,27 @@ def _launch_grouped_fixed(workspace: GroupedWorkspace, cfg: KernelConfig, dtype_
         return splits
     lib = _native.library()
     m, k, n = workspace.shapes[0]
-    status = lib.moegemm_grouped_gemm(
+    stream = _native.current_stream_handle(workspace.a[0].device)
+    args = (
         workspace.a_ptrs.data_ptr(), workspace.b_ptrs.data_ptr(), workspace.c_ptrs.data_ptr(),
         workspace.dims.data_ptr(), workspace.strides.data_ptr(),
         workspace.problem_count, m, n, k, 1 if workspace.homogeneous else 0,
         workspace.tile_count_for(cfg), dtype_code, precision,
         cfg.block_m, cfg.block_n, cfg.block_k, cfg.group_size_m, cfg.num_warps, cfg.num_stages,
         _grid_size(workspace, cfg), 1 if _vector_layout(workspace, dtype_code) else 0,
-        _native.current_stream_handle(workspace.a[0].device),
     )
+    if schedule == "stealing":
+        queue = _native.tile_queue(workspace.a[0].device, stream)
+        status = lib.moegemm_grouped_gemm_stealing(*args, queue.data_ptr(), stream)
+    elif schedule == "static":
+        status = lib.moegemm_grouped_gemm(*args, stream)
+    else:
+        raise ValueError(f"tile_schedule must be one of {_native.TILE_SCHEDULES}, got {schedule!r}")
     _native.check(status)
     return 1
 
 
-_GROUPED_AUTOTUNE_CACHE: dict[tuple, KernelConfig] = {}
+_GROUPED_AUTOTUNE_CACHE: dict[tuple, tuple] = {}
 
 
 def launch_grouped(
@@ -376,16 +399,25 @@ def launch_grouped(
     *,
     autotune: bool = True,
     split_k: int | None = None,
+    tile_schedule: str | None = None,
 ) -> None:
     """Launch the persistent grouped kernel (autotuned per workload key, or a fixed config).
 
     ``split_k`` (keyword-only, not in the reference's signature) as for ``launch_matmul``: None
     splits K inside the one launch when a homogeneous 16-bit group has too few tiles to fill the
     CUs; 1 disables it; n forces n.  ``workspace.split_k`` records what ran.
+    ``tile_schedule`` (keyword-only, not in the reference's signature): "static" (tiles pid,
+    pid + grid, ... as the reference's programs take them) or "stealing" (per-XCD tile queues
+    with stealing); None lets the tuner measure both (static without autotuning).
+    ``workspace.tile_schedule`` records what ran.  G == 1 always runs the single GEMM.
     """
-    _require_runtime()
     if split_k is not None and split_k < 1:
         raise ValueError("split_k must be None or a positive integer")
+    if tile_schedule is not None and tile_schedule not in _native.TILE_SCHEDULES:
+        raise ValueError(f"tile_schedule must be None or one of {_native.TILE_SCHEDULES}, got {tile_schedule!r}")
+    if tile_schedule == "stealing" and split_k is not None and split_k > 1:
+        raise ValueError("the work-stealing schedule runs unsplit launches only (split_k must be 1)")
+    _require_runtime()
     cfg = config or workspace.config
     if workspace.problem_count == 1:
         launch_matmul(workspace.a[0], workspace.b[0], workspace.c[0], cfg, input_precision, autotune=autotune,
@@ -393,6 +425,7 @@ def launch_grouped(
         workspace.config = last_matmul_config(cfg) if autotune else cfg
         workspace.scheduler = "single_problem_matmul"
         workspace.split_k = last_matmul_split()
+        workspace.tile_schedule = "static"
         return
     dtype_code = _check_workspace(workspace)
     precision = _native.precision_code(input_precision, dtype_code)
@@ -401,7 +434,7 @@ def launch_grouped(
         key = (
             scheduler, workspace.problem_count, workspace.max_m, workspace.max_n, workspace.max_k,
             workspace.shape_signature, workspace.device_signature, workspace.sm_count, dtype_code, precision,
-            split_k,
+            split_k, tile_schedule,
         )
         tuned = _GROUPED_AUTOTUNE_CACHE.get(key)
         if tuned is None:
@@ -410,14 +443,22 @@ def launch_grouped(
                 problem_count=workspace.problem_count, sm_count=workspace.sm_count, dtype=workspace.a[0].dtype,
             )
             splittable = workspace.homogeneous and _vector_layout(workspace, dtype_code)
-            options = with_split_options(candidates, workspace.tile_count_for, workspace.max_k, workspace.sm_count,
-                                         split_k, splittable)
-            tuned = _tune(options, lambda o: _launch_grouped_fixed(workspace, o[0], dtype_code, precision, o[1]))
+            options = with_schedule_options(
+                with_split_options(candidates, workspace.tile_count_for, workspace.max_k, workspace.sm_count,
+                                   split_k, splittable),
+                tile_schedule,
+            )
+            tuned = _tune(options, lambda o: _launch_grouped_fixed(workspace, o[0], dtype_code, precision, o[1], o[2]))
             _GROUPED_AUTOTUNE_CACHE[key] = tuned
-        cfg, split_k = tuned
-    workspace.split_k = _launch_grouped_fixed(workspace, cfg, dtype_code, precision, split_k)
+        cfg, split_k, schedule = tuned
+    else:
+        schedule = tile_schedule or "static"
+        if schedule == "stealing" and split_k is None:
+            split_k = 1
+    workspace.split_k = _launch_grouped_fixed(workspace, cfg, dtype_code, precision, split_k, schedule)
     workspace.config = cfg
     workspace.scheduler = scheduler
+    workspace.tile_schedule = schedule
 
 
 # ---------------------------------------------------------------------------------------------

@@ -71,19 +71,25 @@ def _validate(mat_a, mat_b, offs, out):
 
 
 def _launch_fixed(mat_a, mat_b, offs, out, rows, k, n, groups, cfg: KernelConfig, dtype_code: int,
-                  precision: int, sm_count: int) -> None:
+                  precision: int, sm_count: int, schedule: str = "static") -> None:
     grid = max(1, min(offsets_tile_bound(rows, groups, n, cfg.block_m, cfg.block_n), sm_count * cfg.cta_multiplier))
-    status = _native.library().moegemm_grouped_mm_offs(
+    stream = _native.current_stream_handle(mat_a.device)
+    args = (
         mat_a.data_ptr(), mat_b.data_ptr(), out.data_ptr(), offs.data_ptr(), groups, rows, n, k,
         mat_a.stride(0), mat_b.stride(0), mat_b.stride(1), out.stride(0), dtype_code, precision,
         cfg.block_m, cfg.block_n, cfg.block_k, cfg.group_size_m, cfg.num_warps, cfg.num_stages, grid,
-        _native.current_stream_handle(mat_a.device),
     )
+    if schedule == "stealing":
+        queue = _native.tile_queue(mat_a.device, stream)
+        status = _native.library().moegemm_grouped_mm_offs_stealing(*args, queue.data_ptr(), stream)
+    else:
+        status = _native.library().moegemm_grouped_mm_offs(*args, stream)
     _native.check(status)
 
 
-_OFFSETS_AUTOTUNE_CACHE: dict[tuple, KernelConfig] = {}
+_OFFSETS_AUTOTUNE_CACHE: dict[tuple, tuple[KernelConfig, str]] = {}
 _LAST_CONFIG: list[KernelConfig | None] = [None]
+_LAST_SCHEDULE: list[str] = ["static"]
 
 
 def last_grouped_mm_config() -> KernelConfig | None:
@@ -91,17 +97,25 @@ def last_grouped_mm_config() -> KernelConfig | None:
     return _LAST_CONFIG[0]
 
 
+def last_grouped_mm_schedule() -> str:
+    """Tile schedule ("static" or "stealing") of the most recent ``grouped_mm`` call."""
+    return _LAST_SCHEDULE[0]
+
+
 def grouped_mm(mat_a, mat_b, offs, *, out=None, config: KernelConfig | None = None,
-               input_precision: str = "ieee", autotune: bool = True):
+               input_precision: str = "ieee", autotune: bool = True, tile_schedule: str | None = None):
     """C = per-group A @ B[e] over the expert-sorted layout; returns ``out`` (allocated if None).
 
     With ``autotune=True`` and no ``config``, the first call per (rows, K, N, G, strides, dtype)
     key measures the candidate tiles on these operands; later calls are a cache lookup plus one
     kernel launch.  The tuning key does not include ``offs``: the candidates are ranked for an
-    even split of ``rows`` over the groups.
+    even split of ``rows`` over the groups.  ``tile_schedule``: "static", "stealing" (per-XCD
+    work-stealing tile queues), or None to let the tuner measure both (static otherwise).
     """
     import torch
 
+    if tile_schedule is not None and tile_schedule not in _native.TILE_SCHEDULES:
+        raise ValueError(f"tile_schedule must be None or one of {_native.TILE_SCHEDULES}, got {tile_schedule!r}")
     rows, k, n, groups = _validate(mat_a, mat_b, offs, out)
     _require_runtime()
     if out is None:
@@ -113,22 +127,24 @@ def grouped_mm(mat_a, mat_b, offs, *, out=None, config: KernelConfig | None = No
     sm_count = _device_signature(mat_a.device) % 1000
     mean_m = max(1, rows // groups)
 
-    def launch(cfg):
-        _launch_fixed(mat_a, mat_b, offs, out, rows, k, n, groups, cfg, dtype_code, precision, sm_count)
+    def launch(option):
+        _launch_fixed(mat_a, mat_b, offs, out, rows, k, n, groups, option[0], dtype_code, precision, sm_count,
+                      option[1])
 
     if config is not None or not autotune:
-        cfg = config or select_config(mean_m, n, k, mat_a.dtype)
+        option = (config or select_config(mean_m, n, k, mat_a.dtype), tile_schedule or "static")
     else:
         key = (rows, k, n, groups, tuple(mat_a.stride()), tuple(mat_b.stride()), tuple(out.stride()),
-               dtype_code, precision, _device_signature(mat_a.device))
-        cfg = _OFFSETS_AUTOTUNE_CACHE.get(key)
-        if cfg is None:
+               dtype_code, precision, _device_signature(mat_a.device), tile_schedule)
+        option = _OFFSETS_AUTOTUNE_CACHE.get(key)
+        if option is None:
             candidates = grouped_candidate_configs(mean_m, n, k, problem_count=max(groups, 2), sm_count=sm_count,
                                                    dtype=mat_a.dtype)
-            cfg = _tune(candidates, launch)
-            _OFFSETS_AUTOTUNE_CACHE[key] = cfg
-    launch(cfg)
-    _LAST_CONFIG[0] = cfg
+            schedules = _native.TILE_SCHEDULES if tile_schedule is None else (tile_schedule,)
+            option = _tune([(cfg, schedule) for cfg in candidates for schedule in schedules], launch)
+            _OFFSETS_AUTOTUNE_CACHE[key] = option
+    launch(option)
+    _LAST_CONFIG[0], _LAST_SCHEDULE[0] = option
     return out
 
 
@@ -144,6 +160,7 @@ class OffsetsWorkspace:
     device_signature: int = 0
     operation: str = "gemm"
     scheduler: str = "not_launched"
+    tile_schedule: str = "static"
 
     @property
     def problem_count(self) -> int:
@@ -203,14 +220,16 @@ def build_offsets_workspace(
 
 
 def launch_grouped_offsets(workspace: OffsetsWorkspace, input_precision: str = "ieee",
-                           config: KernelConfig | None = None, *, autotune: bool = True) -> None:
-    """One persistent kernel over the workspace; records the config used and the scheduler name.
+                           config: KernelConfig | None = None, *, autotune: bool = True,
+                           tile_schedule: str | None = None) -> None:
+    """One persistent kernel over the workspace; records the config, scheduler name and tile schedule.
 
     Like ``launch_grouped``: with ``autotune=True`` the per-workload tuner picks the config (an
     explicit ``config`` is ignored); otherwise ``config`` (or the workspace's) runs as given.
     """
     grouped_mm(workspace.mat_a, workspace.mat_b, workspace.offs, out=workspace.output,
                config=None if autotune else (config or workspace.config),
-               input_precision=input_precision, autotune=autotune)
+               input_precision=input_precision, autotune=autotune, tile_schedule=tile_schedule)
     workspace.config = last_grouped_mm_config()
     workspace.scheduler = "offsets_persistent"
+    workspace.tile_schedule = last_grouped_mm_schedule()

@@ -429,3 +429,29 @@ def test_offsets_rows_need_the_offsets_scheduler():
     assert not _moe_execution_contract_valid({**row, "scheduler": "homogeneous_persistent"})
     assert not _moe_execution_contract_valid({**GROUPED_ROW, "scheduler": "offsets_persistent"})
     assert not _moe_execution_contract_valid({**row, "launches_per_iteration": "2"})
+
+
+def test_schedule_options_pair_unsplit_candidates_with_both_schedules():
+    from kernels.grouped_gemm import with_schedule_options
+
+    a, b = KernelConfig(16, 256, 64, 8, 4, 4, 1), KernelConfig(64, 128, 64, 8, 4, 4, 1)
+    options = [(a, 1), (a, 4), (b, 1)]
+    assert with_schedule_options(options, None) == [(a, 1, "static"), (a, 1, "stealing"), (a, 4, "static"),
+                                                    (b, 1, "static"), (b, 1, "stealing")]
+    assert with_schedule_options(options, "static") == [(a, 1, "static"), (a, 4, "static"), (b, 1, "static")]
+    assert with_schedule_options(options, "stealing") == [(a, 1, "stealing"), (b, 1, "stealing")]
+
+
+def test_tile_schedule_is_validated_before_touching_a_gpu():
+    from kernels.grouped_gemm import launch_grouped
+    from kernels.grouped_mm import grouped_mm
+
+    workspace = build_grouped_workspace([(8, 16, 32)] * 2, torch.bfloat16, device="cpu")
+    with pytest.raises(ValueError, match="tile_schedule"):
+        launch_grouped(workspace, tile_schedule="dynamic")
+    with pytest.raises(ValueError, match="unsplit"):
+        launch_grouped(workspace, tile_schedule="stealing", split_k=2)
+    a = torch.zeros((8, 16), dtype=torch.bfloat16)
+    b = torch.zeros((2, 16, 8), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="tile_schedule"):
+        grouped_mm(a, b, torch.tensor([4, 8], dtype=torch.int32), tile_schedule="dynamic")

@@ -162,3 +162,17 @@ def test_splitk_entry_rejects_more_tiles_than_counters_without_launching():
     status = lib.moegemm_matmul_splitk(256, 256, 256, m, n, k, k, 1, n, 1, n, 1, _native.DTYPE_BF16,
                                        16, 64, 128, 1, 4, 4, 2, 0, None, 0, None)
     assert status == _native.ERR_INVALID and "output tiles" in _native.last_error()
+
+
+def test_stealing_entries_reject_a_missing_or_misaligned_queue_without_launching():
+    lib = _native.library()
+    args = (1, 1, 1, 1, 1, 4, 16, 64, 64, 1, 4, _native.DTYPE_BF16, 0, 16, 64, 128, 1, 4, 4, 4, 1)
+    assert lib.moegemm_grouped_gemm_stealing(*args, None, None) == _native.ERR_INVALID
+    assert "tile queue" in _native.last_error()
+    assert lib.moegemm_grouped_gemm_stealing(*args, 4, None) == _native.ERR_INVALID
+    assert "256-byte aligned" in _native.last_error()
+    offs_args = (256, 256, 256, 256, 2, 16, 64, 64, 64, 64 * 64, 64, 64, _native.DTYPE_BF16, 0, 16, 64, 128, 1, 4, 4, 4)
+    assert lib.moegemm_grouped_mm_offs_stealing(*offs_args, None, None) == _native.ERR_INVALID
+    assert "tile queue" in _native.last_error()
+    assert lib.moegemm_grouped_mm_offs_stealing(*offs_args, 260, None) == _native.ERR_INVALID
+    assert "256-byte aligned" in _native.last_error()
