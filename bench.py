@@ -225,6 +225,9 @@ def main(argv=None) -> int:
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--kernel-config", metavar="BM,BN,BK,WARPS,STAGES,GROUP_M,MULT", default=None,
                         help="pin the headline kernel config instead of autotuning (counter passes)")
+    parser.add_argument("--case", metavar="PROJ,PAR,M", default=None,
+                        help="only time one DSV3 case (e.g. W1,EP,8), print its row and exit (profiling); "
+                             "--kernel-config pins its kernel")
     parser.add_argument("--copy-calibration", type=int, metavar="MIB", default=0,
                         help="only run a plain device copy of MIB MiB (HBM counter calibration) and exit")
     args = parser.parse_args(argv)
@@ -253,15 +256,31 @@ def main(argv=None) -> int:
 
         bm, bn, bk, warps, stages, group, mult = (int(v) for v in args.kernel_config.split(","))
         pinned = KernelConfig(bm, bn, bk, group, warps, stages, mult)
+    if args.case:
+        projection, parallel_type, m = args.case.split(",")
+        if projection not in ("W1", "W2") or parallel_type not in ("EP", "TP"):
+            raise SystemExit("--case takes PROJ,PAR,M with PROJ in W1/W2 and PAR in EP/TP")
+        row = _case(projection, parallel_type, int(m), args.steps, args.warmup, pinned=pinned)
+        print(json.dumps(row))
+        return 0 if row["correct"] else 1
     headline = _case("W1", "EP", 512, args.steps, args.warmup, pinned=pinned)
     cases = []
     if not args.no_cases:
         for projection, parallel_type, m in (("W1", "EP", 8), ("W1", "TP", 512), ("W1", "TP", 8),
-                                            ("W2", "EP", 512), ("W2", "TP", 512), ("W2", "EP", 8)):
+                                            ("W2", "EP", 512), ("W2", "TP", 512), ("W2", "EP", 8),
+                                            ("W2", "TP", 8)):
             cases.append(_case(projection, parallel_type, m, max(5, args.steps // 2), 2))
         cases.append(_swiglu_case(512, max(5, args.steps // 2), 2))
     traffic = _traffic_from_profiles(headline["case"])
     tp = next((c for c in cases if c["case"] == "dsv3_w1_tp_me512"), None)
+    by_case = {c["case"]: c for c in cases + [headline]}
+    # TP TFLOP/s over EP TFLOP/s at equal per-rank FLOPs (the reference's EP/TP comparison).
+    ep_tp = {}
+    for projection in ("w1", "w2"):
+        for m in (8, 512):
+            ep, tp_case = by_case.get(f"dsv3_{projection}_ep_me{m}"), by_case.get(f"dsv3_{projection}_tp_me{m}")
+            if ep and tp_case:
+                ep_tp[f"{'w13' if projection == 'w1' else 'w2'}_me{m}"] = tp_case["tflops"] / ep["tflops"]
     line = {
         "metric": METRIC,
         "value": headline["tflops"],
@@ -288,6 +307,7 @@ def main(argv=None) -> int:
         "correct": headline["correct"],
         "normwise_error_sampled": headline["normwise_error_sampled"],
         "ep_tp_ratio_w13_me512": (tp["tflops"] / headline["tflops"]) if tp else None,
+        "ep_tp_ratios": ep_tp,
         "cases": cases,
     }
     if not args.no_cpu:
