@@ -172,6 +172,20 @@ def _swiglu_case(m: int, steps: int, warmup: int, seed: int = 1234) -> dict:
     return row
 
 
+def _mfma_busy_from_profiles(case: str):
+    """MFMA busy fraction and GFX clock recorded by a committed rocprofv3 counter summary, if any."""
+    path = REPO / "profiles" / f"{case}_mfma_busy.md"
+    if not path.exists():
+        return None
+    text = path.read_text()
+    busy = re.search(r"mfma_busy_frac:\s*([0-9.]+)", text)
+    clock = re.search(r"gfx_clock_ghz:\s*([0-9.]+)", text)
+    if not busy or not clock:
+        return None
+    return {"busy_frac": float(busy.group(1)), "gfx_clock_ghz": float(clock.group(1)),
+            "source": f"profiles/{path.name}"}
+
+
 def _traffic_from_profiles(case: str):
     """HBM bytes per launch recorded by a committed rocprofv3 counter summary, if any."""
     path = REPO / "profiles" / f"{case}_hbm_traffic.md"
@@ -304,6 +318,7 @@ def main(argv=None) -> int:
             "bound": "mfma", "achieved": headline["tflops"], "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
             "frac": headline["tflops"] / PEAK_BF16_TFLOPS, "traffic": traffic,
         },
+        "mfma_counters": _mfma_busy_from_profiles(headline["case"]),
         "correct": headline["correct"],
         "normwise_error_sampled": headline["normwise_error_sampled"],
         "ep_tp_ratio_w13_me512": (tp["tflops"] / headline["tflops"]) if tp else None,
