@@ -32,6 +32,15 @@
 //    re-arms it (writes 0), fences (device-scope acquire; the other units skip it, so a tile
 //    costs one cache invalidation) and sums all partials of the tile in split order —
 //    the same order whichever unit is last, so results are deterministic — then casts and stores C.
+//  * C epilogue through LDS (STAGED_OK tiles): the 32x32 / 16x16 accumulator layout leaves each
+//    lane 4 consecutive columns of one row, so direct stores write 8 bytes per row per lane and one
+//    store instruction touches 32 (or 16) rows.  Instead each wave converts its WTM x WTN sub-tile
+//    to 16-bit and writes it to the LDS slots that only it fills by DMA (slot j of every stage
+//    belongs to wave j % NW: once the wave's own copies have landed and the K loop is over, no
+//    other wave reads or writes them), row-major with the 16-byte chunk index XOR-swizzled by the
+//    row, then reads it back 16 bytes per lane along rows, so every store instruction writes whole
+//    row segments (8 rows x 128 bytes for a 64-column sub-tile).  The next tile's copies into
+//    those slots are issued by the same wave after its reads have returned.
 // Preconditions (checked by the host before choosing this variant): fp16/bf16, unit inner strides,
 // row pitches and the K, N extents multiples of 8 elements, every matrix < 2 GiB.
 #pragma once
@@ -106,6 +115,12 @@ struct FastTile {
   static constexpr int RPB = 64 / CB;             // B rows per issue
   static constexpr int CPW = WTN / 8;             // B chunks per wave column block
   static constexpr bool SWIGLU_OK = FN % 2 == 0;  // gate and up fragments pair up inside a wave
+  // Staged C epilogue: 16-bit rows of ROWB bytes, whole rows per 1 KiB slot, and the wave's
+  // sub-tile fits the slots it owns (XMIN per stage when every wave issues the same copies).
+  static constexpr int ROWB = WTN * 2;
+  static constexpr int ROW_CHUNKS = ROWB / 16;
+  static constexpr bool STAGED_OK = IA % NW == 0 && IB % NW == 0 && ROWB >= 32 && 1024 % ROWB == 0 &&
+                                    WTM * ROWB <= STAGES * XMIN * 1024 && (WTM * ROWB) % 1024 == 0;
   static constexpr int PREFIX = 512;
   static constexpr int PREFIX_OFFSET = STAGES * STAGE_BYTES;
   static constexpr int LDS_BYTES = PREFIX_OFFSET + (PREFIX + 1) * 4 + NT * 4;
@@ -337,8 +352,61 @@ struct FastTile {
     }
   }
 
+  // LDS byte offset (from the tile's LDS base) of the s-th 1 KiB slot this wave fills by DMA:
+  // per stage, its A slots then its B slots, in issue order.
+  __device__ static __forceinline__ int owned_slot(int s, int wave) {
+    constexpr int PA = IA / NW;
+    const int stage = s / XMIN, t = s % XMIN;
+    return stage * STAGE_BYTES + (t < PA ? (wave + t * NW) * 1024 : A_BYTES + (wave + (t - PA) * NW) * 1024);
+  }
+
+  // Staged C epilogue (see the header comment).  Row r of the wave's sub-tile occupies bytes
+  // [r * ROWB, (r + 1) * ROWB) of its slot sequence; 16-byte chunk c of the row sits at c ^ (r % ROW_CHUNKS).
+  __device__ static __forceinline__ void staged_store(const acc_t (&acc)[FM][FN], const ProblemDesc& pd, int m0,
+                                                      int n0, int wave_m, int wave_n, char* smem) {
+    static_assert(STAGED_OK, "tile cannot stage its C sub-tile");
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    // The caller has waited for this wave's copies (the zero-filled slices past K included).
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      const int r = fm * MI + (lane % MI);
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int q = 0; q < ACC / 4; ++q) {
+          const int c = fn * MI + ((MI == 32) ? (q * 8 + (lane >> 5) * 4) : ((lane >> 4) * 4));
+          const int lin = r * ROWB + (((c >> 3) ^ (r % ROW_CHUNKS)) << 4) + (c & 7) * 2;
+          const f32x4_t v = {acc[fm][fn][q * 4 + 0], acc[fm][fn][q * 4 + 1], acc[fm][fn][q * 4 + 2],
+                             acc[fm][fn][q * 4 + 3]};
+          store4_lds<E>(smem + owned_slot(lin >> 10, wave) + (lin & 1023), v);
+        }
+    }
+    compiler_fence();
+    const bool c16 = ((reinterpret_cast<uintptr_t>(pd.c) & 15) == 0) && (pd.scm & 7) == 0;
+    constexpr int RPI = 1024 / ROWB;  // rows per 1 KiB read
+#pragma unroll
+    for (int j = 0; j < WTM * ROWB / 1024; ++j) {
+      const int r = j * RPI + lane / ROW_CHUNKS, chunk = lane % ROW_CHUNKS;
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(smem + owned_slot(j, wave) +
+                                                          (r % RPI) * ROWB + ((chunk ^ (r % ROW_CHUNKS)) << 4));
+      const int gm = m0 + wave_m * WTM + r, gn = n0 + wave_n * WTN + chunk * 8;
+      if (gm < pd.m && gn < pd.n) {
+        char* dst = pd.c + ((int64_t)gm * pd.scm + gn) * 2;
+        if (c16) {
+          *MOEGEMM_GLOBAL(u32x4_t, dst) = v;
+        } else {
+          *MOEGEMM_GLOBAL(u32x2_t, dst) = u32x2_t{v[0], v[1]};
+          *MOEGEMM_GLOBAL(u32x2_t, dst + 8) = u32x2_t{v[2], v[3]};
+        }
+      }
+    }
+  }
+
+  // Stores the tile (C, the SwiGLU output, or split-K partials).  The wave's copies must have
+  // landed (the staged epilogue reuses its LDS slots).
   __device__ static __forceinline__ void store_tile(const acc_t (&acc)[FM][FN], const ProblemDesc& pd, int m0,
-                                                    int n0, int wave_m, int wave_n) {
+                                                    int n0, int wave_m, int wave_n, char* smem) {
     const int lane = threadIdx.x & 63;
     if (pd.splits > 1) {
       split_store(acc, pd, m0, n0, wave_m, wave_n);
@@ -371,6 +439,10 @@ struct FastTile {
       }
     } else {
       if (pd.swiglu) return;  // the host never selects this tile for the epilogue; store nothing
+    }
+    if constexpr (STAGED_OK) {
+      staged_store(acc, pd, m0, n0, wave_m, wave_n, smem);
+      return;
     }
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
@@ -459,7 +531,7 @@ struct FastTile {
     compiler_fence();
     __builtin_amdgcn_s_barrier();
     compiler_fence();
-    store_tile(acc, pd, m0, n0, wave_m, wave_n);
+    store_tile(acc, pd, m0, n0, wave_m, wave_n, smem);
   }
 };
 

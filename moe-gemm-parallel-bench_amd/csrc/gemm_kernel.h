@@ -178,6 +178,23 @@ __device__ __forceinline__ void store4<EF32>(char* dst, f32x4_t v) {
   *MOEGEMM_GLOBAL(f32x4_t, dst) = v;
 }
 
+// Four fp32 values converted to the 16-bit type, written to LDS (8 bytes).
+template <class E>
+__device__ __forceinline__ void store4_lds(char* dst, f32x4_t v) {
+  static_assert(E::dtype != DT_F32, "16-bit staging only");
+  if constexpr (E::dtype == DT_BF16) {
+    typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+    bf16x4_t o;
+    o[0] = (__bf16)v[0]; o[1] = (__bf16)v[1]; o[2] = (__bf16)v[2]; o[3] = (__bf16)v[3];
+    *reinterpret_cast<bf16x4_t*>(dst) = o;
+  } else {
+    typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+    f16x4_t o;
+    o[0] = (_Float16)v[0]; o[1] = (_Float16)v[1]; o[2] = (_Float16)v[2]; o[3] = (_Float16)v[3];
+    *reinterpret_cast<f16x4_t*>(dst) = o;
+  }
+}
+
 template <class E>
 __device__ __forceinline__ void store1(char* dst, float v);
 template <>

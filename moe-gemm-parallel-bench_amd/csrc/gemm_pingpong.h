@@ -20,8 +20,10 @@
 // Group 0 executes one extra barrier after its last compute phase (storing its outputs first,
 // except for split-K units, whose epilogue synchronises the workgroup and so runs after it) so
 // both groups pass the same number of barriers per tile.  Copies of slices past K read
-// zeros into buffers nobody reads; a wave's copies complete in issue order and every LDS slot is
-// always written by the same wave, so the next tile's prologue needs no drain.
+// zeros into buffers nobody reads; every LDS slot is always written by the same wave, which waits
+// for its own copies before its epilogue (the staged C store reuses its slots).  When group 0
+// stages C after barrier 2K, group 1 has finished its last fragment reads (before that barrier),
+// and each wave touches only its own slots.
 #pragma once
 
 #include "gemm_fast.h"
@@ -92,16 +94,19 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
       if (!second) wait_vmcnt<(STAGES - 2) * XMIN>();
       phase_barrier();
     }
-    before_store();  // before the C stores, as in FastTile
+    // This wave's remaining copies (zero-filled slices past K) land before the epilogue, which may
+    // stage C in the wave's own LDS slots; then the hook, as in FastTile.
+    wait_vmcnt<0>();
+    before_store();
     if (pd.splits > 1) {
       // The split epilogue has workgroup barriers of its own: align the groups first.
       if (!second) phase_barrier();
-      Base::store_tile(acc, pd, m0, n0, wave_m, wave_n);
+      Base::store_tile(acc, pd, m0, n0, wave_m, wave_n, smem);
     } else if (!second) {
-      Base::store_tile(acc, pd, m0, n0, wave_m, wave_n);
+      Base::store_tile(acc, pd, m0, n0, wave_m, wave_n, smem);
       phase_barrier();
     } else {
-      Base::store_tile(acc, pd, m0, n0, wave_m, wave_n);
+      Base::store_tile(acc, pd, m0, n0, wave_m, wave_n, smem);
     }
   }
 };
