@@ -53,6 +53,7 @@ _MENU_16BIT: tuple[tuple[int, int, int, int, int], ...] = (
     (32, 256, 64, 4, 4), (32, 128, 64, 4, 4), (32, 128, 128, 4, 3),
     (16, 256, 64, 4, 4), (16, 256, 128, 4, 2), (16, 128, 128, 4, 4),
     (16, 64, 128, 4, 4), (16, 64, 128, 4, 7),
+    (16, 256, 64, 4, 2), (32, 256, 64, 4, 2), (128, 128, 64, 4, 2), (64, 128, 64, 4, 2),
 )
 _MENU_F32: tuple[tuple[int, int, int, int, int], ...] = (
     (128, 128, 32, 4, 2), (64, 64, 32, 4, 2), (32, 64, 32, 4, 2),
@@ -402,7 +403,9 @@ def _warm_clocks(launch, budget_ms: float = 100.0) -> None:
 
 
 def _tune(candidates, launch):
-    """Hot-time every candidate (graph replays, bounded) after a clock warm-up; re-time the best three."""
+    """Hot-time every candidate (graph replays, bounded) after a clock warm-up, then re-time the best
+    three interleaved (three rounds of A, B, C) and keep the lowest median, so a clock drift during
+    tuning shifts every finalist alike instead of favouring whichever ran at the better moment."""
     candidates = list(candidates)
     measured = []
     warmed = False
@@ -418,5 +421,10 @@ def _tune(candidates, launch):
     if not measured:
         raise RuntimeError("every autotune candidate failed to launch")
     measured.sort(key=lambda item: item[0])
-    finalists = [(hot_autotune_bench(lambda cfg=cfg: launch(cfg), (0.5,))[0], cfg) for _, cfg in measured[:3]]
-    return min(finalists, key=lambda item: item[0])[1]
+    finalists = [cfg for _, cfg in measured[:3]]
+    rounds: list[list[float]] = [[] for _ in finalists]
+    for _ in range(3):
+        for index, cfg in enumerate(finalists):
+            rounds[index].append(hot_autotune_bench(lambda cfg=cfg: launch(cfg), (0.5,))[0])
+    medians = [sorted(times)[1] for times in rounds]
+    return finalists[medians.index(min(medians))]
