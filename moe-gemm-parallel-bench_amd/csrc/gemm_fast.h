@@ -124,6 +124,10 @@ struct FastTile {
   static constexpr int PREFIX = 512;
   static constexpr int PREFIX_OFFSET = STAGES * STAGE_BYTES;
   static constexpr int LDS_BYTES = PREFIX_OFFSET + (PREFIX + 1) * 4 + NT * 4;
+  // Two-stage narrow tiles are meant to run two workgroups per CU (one's prologue under the other's
+  // work): that needs two waves per SIMD, i.e. at most 256 registers per wave, which the kernel
+  // asks the compiler for.  Every other tile takes what it needs.
+  static constexpr int WAVES_PER_EU = (STAGES == 2 && 2 * LDS_BYTES <= 160 * 1024 && BM * BN <= 32 * 256) ? 2 : 1;
 
   static_assert(STAGES >= 2, "need at least double buffering");
   static_assert(A_BYTES % 1024 == 0 && B_BYTES % 1024 == 0, "stages must be whole 1 KiB DMA issues");

@@ -254,6 +254,7 @@ struct GemmTile {
   static constexpr int PREFIX = 1024;  // problems per prefix-sum chunk (generic mode)
   static constexpr int PREFIX_OFFSET = 2 * STAGE_BYTES;
   static constexpr int LDS_BYTES = PREFIX_OFFSET + (PREFIX + 1) * 4 + NT * 4;
+  static constexpr int WAVES_PER_EU = 1;
 
   static_assert(BM % WM == 0 && BN % WN == 0, "tile must split evenly over waves");
   static_assert(WTM % MI == 0 && WTN % MI == 0, "wave tile must be a multiple of the MFMA tile");
@@ -648,7 +649,8 @@ struct TileQueue {
 };
 
 template <class T>
-__global__ void __launch_bounds__(T::NT) grouped_gemm_kernel(KParams p) {
+__global__ void __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WAVES_PER_EU)))
+grouped_gemm_kernel(KParams p) {
   __shared__ __attribute__((aligned(16))) char smem[T::LDS_BYTES];
   int* s_pref = reinterpret_cast<int*>(smem + T::PREFIX_OFFSET);
   int* s_tot = s_pref + T::PREFIX + 1;
