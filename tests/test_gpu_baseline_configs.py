@@ -1,7 +1,7 @@
 """GPU tests at the BASELINE configurations' full per-rank sizes, plus graph capture and timing.
 
-Full-size checks use properties that do not depend on size (the exact-integer check runs on all 36
-MoE cases of BASELINE configs[1..3], the random check on a representative subset):
+Full-size checks, on all 36 MoE cases of BASELINE configs[1..3], use properties that do not depend
+on size:
   * exact-integer known answers on every expert (A = 1, B_e = e + 1 => C_e = K (e + 1), exact in
     the fp32 accumulator and representable in bf16/fp16 for these K) - catches any wrong index,
     missing tile, duplicated tile or tail error anywhere in the group;
@@ -23,24 +23,8 @@ pytestmark = pytest.mark.gpu
 
 NORMWISE = {torch.bfloat16: 1e-2, torch.float16: 2e-3}
 
-# (name, projection, parallel, M_e, H, F, E, P, dtype)
-CASES = [
-    ("dsv3_w1_ep_me8", "W1", "EP", 8, 7168, 2048, 256, 8, torch.bfloat16),
-    ("dsv3_w1_ep_me512", "W1", "EP", 512, 7168, 2048, 256, 8, torch.bfloat16),
-    ("dsv3_w1_tp_me64", "W1", "TP", 64, 7168, 2048, 256, 8, torch.bfloat16),
-    ("dsv3_w2_ep_me64", "W2", "EP", 64, 7168, 2048, 256, 8, torch.bfloat16),
-    ("dsv3_w2_tp_me512", "W2", "TP", 512, 7168, 2048, 256, 8, torch.bfloat16),
-    ("mixtral_w1_ep_me16", "W1", "EP", 16, 4096, 14336, 8, 8, torch.bfloat16),
-    ("mixtral_w2_ep_me128", "W2", "EP", 128, 4096, 14336, 8, 8, torch.bfloat16),
-    ("mixtral_w1_tp_me1024", "W1", "TP", 1024, 4096, 14336, 8, 8, torch.bfloat16),
-    ("mixtral_w2_tp_me16", "W2", "TP", 16, 4096, 14336, 8, 8, torch.bfloat16),
-    ("qwen3_w1_ep_me4", "W1", "EP", 4, 2048, 768, 128, 4, torch.float16),
-    ("qwen3_w1_tp_me256", "W1", "TP", 256, 2048, 768, 128, 4, torch.float16),
-    ("qwen3_w2_tp_me32", "W2", "TP", 32, 2048, 768, 128, 4, torch.float16),
-]
-
-
-# Every MoE case of BASELINE configs[1..3]: 3 models x {W1, W2} x {EP, TP} x their M_e sweep.
+# Every MoE case of BASELINE configs[1..3]: 3 models x {W1, W2} x {EP, TP} x their M_e sweep, as
+# (name, projection, parallel, M_e, H, F, E, P, dtype).
 _MODELS = (("dsv3", (8, 64, 512), 7168, 2048, 256, 8, torch.bfloat16),
            ("mixtral", (16, 128, 1024), 4096, 14336, 8, 8, torch.bfloat16),
            ("qwen3", (4, 32, 256), 2048, 768, 128, 4, torch.float16))
@@ -86,7 +70,7 @@ def test_full_size_exact_integer_every_expert(case):
         assert torch.all(c == expected), f"{name}: expert {index} wrong with {workspace.config}"
 
 
-@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+@pytest.mark.parametrize("case", ALL_CASES, ids=[c[0] for c in ALL_CASES])
 def test_full_size_random_sampled_against_references(case):
     from kernels.grouped_gemm import launch_grouped
 
