@@ -170,6 +170,16 @@ _SPLITK_WORKSPACES: dict[tuple[int, int], list] = {}
 _SPLITK_MIN_BYTES = 32 << 20
 
 
+def _refuse_allocation_under_capture(what: str) -> None:
+    """A buffer made inside graph capture would be zeroed only when the graph replays, so an eager
+    launch on that stream before the first replay would read stale counters: refuse instead."""
+    import torch
+
+    if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+        raise RuntimeError(f"the {what} for this stream does not exist yet and cannot be created during graph "
+                           "capture; make the first call on this stream outside capture")
+
+
 def splitk_workspace(device, stream_handle: int, nbytes: int):
     """A zero-initialised uint8 device tensor of at least ``nbytes`` for this device and stream."""
     import torch
@@ -177,6 +187,7 @@ def splitk_workspace(device, stream_handle: int, nbytes: int):
     key = (torch.device(device).index or 0, int(stream_handle))
     held = _SPLITK_WORKSPACES.setdefault(key, [])
     if not held or held[-1].numel() < nbytes:
+        _refuse_allocation_under_capture("split-K workspace")
         held.append(torch.zeros(max(nbytes, _SPLITK_MIN_BYTES), dtype=torch.uint8, device=device))
     return held[-1]
 
@@ -195,6 +206,7 @@ def tile_queue(device, stream_handle: int):
     key = (torch.device(device).index or 0, int(stream_handle))
     queue = _TILE_QUEUES.get(key)
     if queue is None:
+        _refuse_allocation_under_capture("work-stealing tile queue")
         queue = torch.zeros(QUEUE_BYTES // 4, dtype=torch.int32, device=device)
         _TILE_QUEUES[key] = queue
     return queue

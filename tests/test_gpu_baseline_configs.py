@@ -132,6 +132,9 @@ def test_launch_grouped_is_graph_capturable_and_replays_match_eager():
     eager = [c.clone() for c in workspace.c]
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        launch_grouped(workspace)  # first call on this stream outside capture (its per-stream buffers)
+    torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
         launch_grouped(workspace)  # cache hit: one kernel launch, captured

@@ -176,3 +176,20 @@ def test_stealing_entries_reject_a_missing_or_misaligned_queue_without_launching
     assert "tile queue" in _native.last_error()
     assert lib.moegemm_grouped_mm_offs_stealing(*offs_args, 260, None) == _native.ERR_INVALID
     assert "256-byte aligned" in _native.last_error()
+
+
+def test_stream_buffers_are_not_created_during_graph_capture(monkeypatch):
+    import torch
+
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: True)
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    with pytest.raises(RuntimeError, match="outside capture"):
+        _native.tile_queue("cpu", 987654321)
+    with pytest.raises(RuntimeError, match="outside capture"):
+        _native.splitk_workspace("cpu", 987654321, 1024)
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+    queue = _native.tile_queue("cpu", 987654321)  # made outside capture: reused afterwards, even under capture
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    assert _native.tile_queue("cpu", 987654321) is queue
+    _native._TILE_QUEUES.pop((0, 987654321))
+    _native._SPLITK_WORKSPACES.pop((0, 987654321), None)
