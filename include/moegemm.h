@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define MOEGEMM_ABI_VERSION 4
+#define MOEGEMM_ABI_VERSION 5
 
 #define MOEGEMM_OK 0
 #define MOEGEMM_ERR_INVALID (-1)   /* bad shape, pointer, dtype or parameter (Python: ValueError) */
@@ -176,6 +176,23 @@ int moegemm_grouped_mm_offs(const void* a, const void* b, void* c, const int32_t
                             int32_t block_m, int32_t block_n, int32_t block_k,
                             int32_t group_size_m, int32_t num_warps, int32_t num_stages,
                             int32_t grid_size, void* stream);
+/*
+ * Packed Gate+Up over the expert-sorted layout with the SwiGLU epilogue: B is [group_count, k, n]
+ * with n = 2F columns [gate | up] per group (the packed W13 weights of reference
+ * kernels/grouped_gemm.py:575-594, stored as the 3-D grouped_mm operand of
+ * kernels/torch_grouped_gemm.py:139-158), and H [rows, F] (row stride stride_hm) receives
+ * silu(A[r0:r1] @ B[e][:, :F]) * (A[r0:r1] @ B[e][:, F:]) for each group, from the fp32 accumulators.
+ * Offsets, clamping and untouched rows as in moegemm_grouped_mm_offs.  No counterpart in the reference
+ * (it keeps the activation outside its timed GEMM, README.md:55-57).  Requires fp16/bf16, the vector
+ * layout, n a multiple of 16 and a tile with moegemm_kernel_swiglu() == 1.
+ */
+int moegemm_grouped_mm_offs_swiglu(const void* a, const void* b, void* h, const int32_t* offs,
+                                   int32_t group_count, int32_t rows, int32_t n, int32_t k,
+                                   int64_t stride_am, int64_t stride_bg, int64_t stride_bk,
+                                   int64_t stride_hm, int32_t dtype, int32_t block_m,
+                                   int32_t block_n, int32_t block_k, int32_t group_size_m,
+                                   int32_t num_warps, int32_t num_stages, int32_t grid_size,
+                                   void* stream);
 /* The same launch with the work-stealing tile scheduler and queue of
  * moegemm_grouped_gemm_stealing; ragged offsets give tiles of unequal cost (partial M tiles). */
 int moegemm_grouped_mm_offs_stealing(const void* a, const void* b, void* c, const int32_t* offs,

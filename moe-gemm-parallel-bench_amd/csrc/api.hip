@@ -353,11 +353,12 @@ int moegemm_kernel_swiglu(int dtype, int index) {
   return t[index].swiglu_ok;
 }
 
+// `swiglu`: B holds [gate | up] (n = 2F columns) and C is H [rows, F] (row stride stride_cm).
 static int offsets_impl(const void* a, const void* b, void* c, const int32_t* offs, int32_t group_count, int32_t rows,
                         int32_t n, int32_t k, int64_t stride_am, int64_t stride_bg, int64_t stride_bk,
                         int64_t stride_cm, int32_t dtype, int32_t input_precision, int32_t block_m, int32_t block_n,
                         int32_t block_k, int32_t group_size_m, int32_t num_warps, int32_t num_stages,
-                        int32_t grid_size, void* queue, void* stream) {
+                        int32_t grid_size, bool swiglu, void* queue, void* stream) {
   const KernelEntry* e = nullptr;
   int rc = check_common(dtype, input_precision, group_size_m, &e, block_m, block_n, block_k, num_warps, num_stages);
   if (rc != MOEGEMM_OK) return rc;
@@ -365,7 +366,17 @@ static int offsets_impl(const void* a, const void* b, void* c, const int32_t* of
   if (group_count <= 0) return fail(MOEGEMM_ERR_INVALID, "group_count must be positive (got %d)", group_count);
   if (rows < 0 || n <= 0 || k <= 0)
     return fail(MOEGEMM_ERR_INVALID, "shape must have rows >= 0 and positive n, k (rows=%d n=%d k=%d)", rows, n, k);
-  if (stride_am < k || stride_bk < n || stride_cm < n || stride_bg < (int64_t)k * stride_bk)
+  const int64_t out_cols = swiglu ? n / 2 : n;
+  if (swiglu) {
+    if (dtype != DT_BF16 && dtype != DT_F16)
+      return fail(MOEGEMM_ERR_INVALID, "the SwiGLU epilogue needs fp16 or bf16 operands");
+    if (!e->swiglu_ok)
+      return fail(MOEGEMM_ERR_INVALID,
+                  "tile %dx%dx%d with %d waves cannot pair gate and up fragments (odd fragments per wave)",
+                  block_m, block_n, block_k, num_warps);
+    if (n % 16) return fail(MOEGEMM_ERR_INVALID, "packed Gate+Up width must be a multiple of 16 (got %d)", n);
+  }
+  if (stride_am < k || stride_bk < n || stride_cm < out_cols || stride_bg < (int64_t)k * stride_bk)
     return fail(MOEGEMM_ERR_INVALID,
                 "strides overlap rows or groups (stride_am=%lld stride_bk=%lld stride_bg=%lld stride_cm=%lld)",
                 (long long)stride_am, (long long)stride_bk, (long long)stride_bg, (long long)stride_cm);
@@ -392,6 +403,7 @@ static int offsets_impl(const void* a, const void* b, void* c, const int32_t* of
   p.group_m = group_size_m;
   p.tf32 = input_precision == MOEGEMM_PRECISION_TF32;
   p.total_tiles = (int32_t)tiles;
+  p.swiglu = swiglu ? 1 : 0;
   const int grid = grid_size <= 0 ? p.total_tiles : (grid_size < p.total_tiles ? grid_size : p.total_tiles);
   // Every group shares the strides, so one check covers all of them; the A resource of a tile spans
   // at most block_m rows, each group's B resource one [k, n] panel.
@@ -400,6 +412,8 @@ static int offsets_impl(const void* a, const void* b, void* c, const int32_t* of
                    (reinterpret_cast<uintptr_t>(a) & 15) == 0 && (reinterpret_cast<uintptr_t>(b) & 15) == 0 &&
                    (reinterpret_cast<uintptr_t>(c) & 7) == 0 && (int64_t)block_m * stride_am * 2 < (int64_t(1) << 31) &&
                    (int64_t)k * stride_bk * 2 < (int64_t(1) << 31);
+  if (swiglu && !vec)
+    return fail(MOEGEMM_ERR_INVALID, "the SwiGLU epilogue needs the vector layout (LDS-DMA kernel)");
   rc = set_queue(p, queue);
   if (rc != MOEGEMM_OK) return rc;
   return launch(e, p, grid, vec, stream);
@@ -412,7 +426,17 @@ int moegemm_grouped_mm_offs(const void* a, const void* b, void* c, const int32_t
                             int32_t num_warps, int32_t num_stages, int32_t grid_size, void* stream) {
   return offsets_impl(a, b, c, offs, group_count, rows, n, k, stride_am, stride_bg, stride_bk, stride_cm, dtype,
                       input_precision, block_m, block_n, block_k, group_size_m, num_warps, num_stages, grid_size,
-                      nullptr, stream);
+                      false, nullptr, stream);
+}
+
+int moegemm_grouped_mm_offs_swiglu(const void* a, const void* b, void* h, const int32_t* offs, int32_t group_count,
+                                   int32_t rows, int32_t n, int32_t k, int64_t stride_am, int64_t stride_bg,
+                                   int64_t stride_bk, int64_t stride_hm, int32_t dtype, int32_t block_m,
+                                   int32_t block_n, int32_t block_k, int32_t group_size_m, int32_t num_warps,
+                                   int32_t num_stages, int32_t grid_size, void* stream) {
+  return offsets_impl(a, b, h, offs, group_count, rows, n, k, stride_am, stride_bg, stride_bk, stride_hm, dtype,
+                      MOEGEMM_PRECISION_IEEE, block_m, block_n, block_k, group_size_m, num_warps, num_stages,
+                      grid_size, true, nullptr, stream);
 }
 
 int moegemm_grouped_mm_offs_stealing(const void* a, const void* b, void* c, const int32_t* offs,
@@ -424,7 +448,7 @@ int moegemm_grouped_mm_offs_stealing(const void* a, const void* b, void* c, cons
   if (!queue) return fail(MOEGEMM_ERR_INVALID, "the work-stealing launch needs a tile queue");
   return offsets_impl(a, b, c, offs, group_count, rows, n, k, stride_am, stride_bg, stride_bk, stride_cm, dtype,
                       input_precision, block_m, block_n, block_k, group_size_m, num_warps, num_stages, grid_size,
-                      queue, stream);
+                      false, queue, stream);
 }
 
 int moegemm_matmul(const void* a, const void* b, void* c, int32_t m, int32_t n, int32_t k, int64_t stride_am,

@@ -12,6 +12,7 @@ from .grouped_mm import (
     OffsetsWorkspace,
     build_offsets_workspace,
     grouped_mm,
+    grouped_mm_swiglu,
     last_grouped_mm_config,
     last_grouped_mm_schedule,
     launch_grouped_offsets,
@@ -43,6 +44,7 @@ __all__ = [
     "build_torch_grouped_workspace",
     "grouped_candidate_configs",
     "grouped_mm",
+    "grouped_mm_swiglu",
     "last_grouped_mm_config",
     "last_grouped_mm_schedule",
     "last_matmul_config",

@@ -15,7 +15,7 @@ from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().with_name("libmoegemm.so")
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 OK = 0
 ERR_INVALID = -1
 ERR_NO_KERNEL = -2
@@ -69,6 +69,11 @@ SIGNATURES = {
     "moegemm_grouped_mm_offs": (
         ctypes.c_int,
         [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i32, _i32,
+         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
+    ),
+    "moegemm_grouped_mm_offs_swiglu": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i32,
          _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
     ),
     "moegemm_grouped_mm_offs_stealing": (

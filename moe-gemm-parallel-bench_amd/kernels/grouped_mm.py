@@ -15,6 +15,8 @@ operands go to the persistent HIP kernel through ``moegemm_grouped_mm_offs``:
   leaves them unspecified too: ``out=None`` allocates with ``torch.empty`` like torch); offsets
   beyond ``rows`` are clamped on the device, so any ``offs`` content is memory-safe (offsets that
   decrease give empty or overlapping groups, whose results are unspecified).
+* ``grouped_mm_swiglu`` is the packed Gate+Up launch over the same layout with the SiLU(gate)*up
+  activation fused into the epilogue (H [rows, F] out; one kernel launch).
 * ``build_offsets_workspace`` / ``launch_grouped_offsets`` mirror the torch provider's workspace
   API for the drivers (same seeded ``normal_() * 0.1`` operands, same 16-byte row padding, same
   ``problem_tensors()`` view of each expert).
@@ -28,7 +30,7 @@ from itertools import accumulate
 
 from . import _native
 from .grouped_gemm import grouped_candidate_configs
-from .matmul import KernelConfig, _device_signature, _require_runtime, _tune, select_config
+from .matmul import KernelConfig, _device_signature, _require_runtime, _tune, config_pool, select_config
 
 
 def offsets_tile_bound(rows: int, group_count: int, n: int, block_m: int, block_n: int) -> int:
@@ -145,6 +147,84 @@ def grouped_mm(mat_a, mat_b, offs, *, out=None, config: KernelConfig | None = No
             _OFFSETS_AUTOTUNE_CACHE[key] = option
     launch(option)
     _LAST_CONFIG[0], _LAST_SCHEDULE[0] = option
+    return out
+
+
+_SWIGLU_OFFSETS_CACHE: dict[tuple, KernelConfig] = {}
+_LAST_SWIGLU_CONFIG: list[KernelConfig | None] = [None]
+
+
+def last_grouped_mm_swiglu_config() -> KernelConfig | None:
+    """Config used by the most recent ``grouped_mm_swiglu`` call."""
+    return _LAST_SWIGLU_CONFIG[0]
+
+
+def grouped_mm_swiglu(mat_a, mat_b, offs, *, out=None, config: KernelConfig | None = None,
+                      autotune: bool = True):
+    """Packed Gate+Up with the SwiGLU activation fused, over the expert-sorted layout.
+
+    ``mat_b`` [G, K, 2F] holds each group's [gate | up] columns (the packed W13 weights of the
+    reference's build_fused_gate_up_workspace, kernels/grouped_gemm.py:575-594, in the 3-D layout
+    of its torch provider).  Returns H [rows, F] with H[r0:r1] = silu(A[r0:r1] @ B[e][:, :F]) *
+    (A[r0:r1] @ B[e][:, F:]) computed from the fp32 accumulators, for r0 = offs[e-1] (0 for e = 0)
+    and r1 = offs[e].  One kernel launch; rows at or past offs[-1] are not written.  fp16/bf16 in
+    the vector layout (16-byte aligned rows, K and F multiples of 8) only (ValueError otherwise).
+    Autotuning as in ``grouped_mm``, over the tiles that can pair gate and up fragments.
+    """
+    import torch
+
+    rows, k, n, groups = _validate(mat_a, mat_b, offs, None)
+    f = n // 2
+    if mat_a.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("the fused SwiGLU epilogue needs fp16 or bf16 operands")
+    if n % 16:
+        raise ValueError(f"packed Gate+Up width must be 2F with F a multiple of 8 (got {n} columns)")
+    if out is not None and (tuple(out.shape) != (rows, f) or out.dtype != mat_a.dtype or out.stride(1) != 1
+                            or out.device != mat_a.device):
+        raise ValueError(f"out must be a [{rows}, {f}] {mat_a.dtype} matrix with unit column stride on the same device")
+    vector = (k % 8 == 0 and mat_a.stride(0) % 8 == 0 and mat_b.stride(1) % 8 == 0 and mat_b.stride(0) % 8 == 0
+              and mat_a.data_ptr() % 16 == 0 and mat_b.data_ptr() % 16 == 0)
+    if not vector:
+        raise ValueError("the fused SwiGLU epilogue needs 16-byte aligned operands with K a multiple of 8")
+    _require_runtime()
+    if out is None:
+        out = torch.empty((rows, f), device=mat_a.device, dtype=mat_a.dtype)
+    if out.stride(0) % 4 or out.data_ptr() % 8:
+        raise ValueError("out rows must be 8-byte aligned")
+    if rows == 0:
+        return out
+    dtype_code = _native.dtype_code(mat_a.dtype)
+    sm_count = _device_signature(mat_a.device) % 1000
+    allowed = _native.swiglu_tiles(dtype_code)
+
+    def launch(cfg):
+        grid = max(1, min(offsets_tile_bound(rows, groups, n, cfg.block_m, cfg.block_n), sm_count * cfg.cta_multiplier))
+        status = _native.library().moegemm_grouped_mm_offs_swiglu(
+            mat_a.data_ptr(), mat_b.data_ptr(), out.data_ptr(), offs.data_ptr(), groups, rows, n, k,
+            mat_a.stride(0), mat_b.stride(0), mat_b.stride(1), out.stride(0), dtype_code,
+            cfg.block_m, cfg.block_n, cfg.block_k, cfg.group_size_m, cfg.num_warps, cfg.num_stages, grid,
+            _native.current_stream_handle(mat_a.device),
+        )
+        _native.check(status)
+
+    if config is not None or not autotune:
+        cfg = config
+        if cfg is None:
+            cfg = next((c for c in config_pool(mat_a.dtype) if c.tile_key in allowed and c.group_size_m == 8), None)
+    else:
+        key = (rows, k, n, groups, tuple(mat_a.stride()), tuple(mat_b.stride()), tuple(out.stride()), dtype_code,
+               _device_signature(mat_a.device))
+        cfg = _SWIGLU_OFFSETS_CACHE.get(key)
+        if cfg is None:
+            mean_m = max(1, rows // groups)
+            ranked = grouped_candidate_configs(mean_m, n, k, problem_count=max(groups, 2), sm_count=sm_count,
+                                               dtype=mat_a.dtype)
+            candidates = [c for c in ranked if c.tile_key in allowed] or \
+                [c for c in config_pool(mat_a.dtype) if c.tile_key in allowed and c.group_size_m == 8][:6]
+            cfg = _tune(candidates, launch)
+            _SWIGLU_OFFSETS_CACHE[key] = cfg
+    launch(cfg)
+    _LAST_SWIGLU_CONFIG[0] = cfg
     return out
 
 

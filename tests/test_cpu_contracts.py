@@ -407,6 +407,17 @@ def test_grouped_mm_validates_before_touching_a_gpu():
         grouped_mm(a, b[:, :8], offs)
 
 
+def test_grouped_mm_swiglu_validates_before_touching_a_gpu():
+    from kernels.grouped_mm import grouped_mm_swiglu
+
+    a = torch.zeros((8, 16), dtype=torch.bfloat16)
+    offs = torch.tensor([4, 8], dtype=torch.int32)
+    with pytest.raises(ValueError):  # host tensors: the kernel path needs a GPU device
+        grouped_mm_swiglu(a, torch.zeros((2, 16, 32), dtype=torch.bfloat16), offs)
+    with pytest.raises(ValueError):
+        grouped_mm_swiglu(a, torch.zeros((2, 16, 32), dtype=torch.bfloat16), offs.long())
+
+
 def test_moe_offsets_mode_is_opt_in(tmp_path):
     base = dict(num_experts=8, parallel_size=4, ffn_size=16, hidden_size=32, topk=1, moe_ms=[1],
                 tokens=None, torch_baseline=False, results_dir=tmp_path)
