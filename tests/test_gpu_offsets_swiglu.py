@@ -5,7 +5,9 @@ H[r0:r1] = silu(A[r0:r1] @ B[e][:, :F]) * (A[r0:r1] @ B[e][:, F:]) per group is 
 tests/test_oracle.py) with the normwise bound max|H - R| / max|R| (bf16 <= 1e-2, fp16 <= 2e-3):
 every tile that can pair gate and up fragments, ragged offsets with an empty group and rows past
 offs[-1] (which must stay untouched), and a DeepSeek-V3 EP W13 shard with ragged routing on sampled
-rows against a float32 torch product.  Unsupported inputs raise ValueError.
+rows against a float32 torch product; and a whole expert FFN on sorted tokens in two launches
+(grouped_mm_swiglu, then grouped_mm for W2 on the same offsets, with an expert that received no
+tokens).  Unsupported inputs raise ValueError.
 """
 
 from __future__ import annotations
@@ -117,3 +119,35 @@ def test_unsupported_inputs_raise_value_error():
     with pytest.raises(ValueError):
         grouped_mm_swiglu(*_operands(16, 64, 256, 2, torch.bfloat16), offs,
                           config=KernelConfig(bm, bn, bk, 8, warps, stages, 1))
+
+
+def test_expert_ffn_on_sorted_tokens_in_two_launches():
+    """Y = W2(silu(X W1) * (X W3)) per expert: grouped_mm_swiglu then grouped_mm on the same offs,
+    against float32 torch on sampled rows (H rounded to bf16 between the launches, as stored)."""
+    from kernels.grouped_mm import grouped_mm, grouped_mm_swiglu
+
+    rng = np.random.default_rng(3)
+    experts, hidden, ffn = 16, 1024, 512
+    sizes = [int(v) for v in rng.integers(0, 200, size=experts)]
+    sizes[3] = 0  # an expert no token was routed to
+    ends = np.cumsum(sizes).tolist()
+    rows = ends[-1]
+    print(f"expert FFN rows={rows} experts={experts} H={hidden} F={ffn}", flush=True)
+    x = torch.randn((rows, hidden), device="cuda", dtype=torch.bfloat16)
+    w13 = torch.randn((experts, hidden, 2 * ffn), device="cuda", dtype=torch.bfloat16) / math.sqrt(hidden)
+    w2 = torch.randn((experts, ffn, hidden), device="cuda", dtype=torch.bfloat16) / math.sqrt(ffn)
+    offs = torch.tensor(ends, device="cuda", dtype=torch.int32)
+    h = grouped_mm_swiglu(x, w13, offs)
+    y = grouped_mm(h, w2, offs)
+    torch.cuda.synchronize()
+    for e in range(experts):
+        if sizes[e] == 0:
+            continue
+        r0 = ends[e] - sizes[e]
+        sample = torch.tensor(sorted({r0, r0 + sizes[e] // 2, ends[e] - 1}), device="cuda")
+        xs = x[sample].float()
+        gate, up = xs @ w13[e, :, :ffn].float(), xs @ w13[e, :, ffn:].float()
+        h_ref = (torch.nn.functional.silu(gate) * up).to(torch.bfloat16).float()
+        y_ref = h_ref @ w2[e].float()
+        assert normwise(h[sample].float().cpu(), h_ref.cpu()) <= 1e-2, f"expert {e}: H"
+        assert normwise(y[sample].float().cpu(), y_ref.cpu()) <= 1e-2, f"expert {e}: Y"
