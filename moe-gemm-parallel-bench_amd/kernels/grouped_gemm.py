@@ -30,7 +30,7 @@ from .matmul import (
     _require_runtime,
     _tune,
     config_pool,
-    diverse_configs,
+    diverse_configs,  # importable from here as in the reference's kernels/grouped_gemm.py
     estimate_seconds,
     last_matmul_config,
     launch_matmul,
