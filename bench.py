@@ -194,6 +194,33 @@ def _traffic_from_profiles(case: str):
     return float(match.group(1)) if match else None
 
 
+def _cpu_torch_mm(seconds_target: float = 5.0) -> dict:
+    """The reference's CPU path for this work, the per-expert torch.mm (benchmark_moe.py:258-266),
+    in bf16 on the host cores over a bounded sample of the same expert GEMM."""
+    import torch
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    generator = torch.Generator().manual_seed(1234)
+    m, k, n = 512, DSV3["hidden"], 2 * DSV3["ffn"]
+    a = (torch.randn((m, k), generator=generator) * 0.1).to(torch.bfloat16)
+    b = (torch.randn((k, n), generator=generator) * 0.1).to(torch.bfloat16)
+    torch.mm(a, b[:, :256])  # warm
+    calls, elapsed = 0, 0.0
+    while elapsed < seconds_target and calls < 4096:
+        t0 = time.perf_counter()
+        torch.mm(a, b)
+        elapsed += time.perf_counter() - t0
+        calls += 1
+    return {
+        "value": calls * 2 * m * k * n / elapsed / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "reference-path torch.mm",
+        "sample": f"{calls} calls of one expert's [512,7168]@[7168,4096] bf16 torch.mm ({elapsed:.1f} s)",
+    }
+
+
 def _cpu_baseline(seconds_target: float = 12.0) -> dict:
     """Oracle blocked GEMM on the host cores over a bounded sample of the workload."""
     import numpy as np
@@ -326,6 +353,7 @@ def main(argv=None) -> int:
     }
     if not args.no_cpu:
         line["cpu_baseline"] = _cpu_baseline()
+        line["cpu_torch_mm"] = _cpu_torch_mm()
     print(json.dumps(line))
     return 0 if headline["correct"] and all(c["correct"] for c in cases) else 1
 
