@@ -134,7 +134,7 @@ struct FastTile {
   static_assert(CA <= 64 && CB <= 64 && 64 % CA == 0 && 64 % CB == 0, "rows must tile a 1 KiB issue");
   static_assert(CB >= 4, "transpose reads need at least 32 columns");
   static_assert(WTM % MI == 0 && WTN % MI == 0 && BK % MIK == 0, "tile shape");
-  static_assert((STAGES - 2) * XMIN < 64, "vmcnt budget");
+  static_assert(STAGES * (QA + QB) < 64, "vmcnt budget: every copy in flight must fit the 6-bit counter");
   static_assert(LDS_BYTES <= 160 * 1024, "LDS budget of one CU");
 
   using acc_t = typename std::conditional<ACC == 16, f32x16_t, f32x4_t>::type;

@@ -1,0 +1,106 @@
+"""GPU tests of workgroups that run several tiles in a row on the static schedule.
+
+Each tile's epilogue stages C in the LDS slots that the next tile's copies refill, so a tile must
+leave nothing behind for its successor.  Exact-integer results (small integers in A and B, so the
+fp32 sums are exact and the store rounds them as the float64 reference rounded to the dtype does)
+are checked for every compiled 16-bit tile at grids that give each workgroup several tiles, with
+ragged M, N and K so that the last tiles store partial rows and columns; NaN guard bands around
+each C catch a store outside it.  Homogeneous groups mix 16-byte-aligned and 8-byte-aligned C
+(whole-row and half-row stores alternate within a launch), and single GEMMs write into a column
+slice of a wider matrix whose other columns must stay untouched.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = (torch.bfloat16, torch.float16)
+GUARD = 4096
+
+
+@pytest.fixture(autouse=True)
+def _gpu_only():
+    if not torch.cuda.is_available():
+        pytest.skip("ROCm GPU unavailable")
+    torch.manual_seed(5)
+
+
+def _ints(shape, dtype):
+    return torch.randint(-2, 3, shape, device="cuda").to(dtype)
+
+
+def _tiles(dtype):
+    from kernels import _native
+
+    return [tuple(row[:5]) for row in _native.compiled_kernels(_native.dtype_code(dtype))]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+def test_homogeneous_every_tile_small_grids_mixed_alignment(dtype):
+    from kernels import _native
+    from kernels.grouped_gemm import _vector_layout, build_grouped_workspace
+
+    groups, m, k, n = 5, 300, 200, 392
+    ws = build_grouped_workspace([(m, k, n)] * groups, dtype, seed=1)
+    storages = []
+    for e in range(groups):
+        ws.a[e].copy_(_ints((m, k), dtype))
+        ws.b[e].copy_(_ints((k, n), dtype))
+        lead = GUARD + (4 if e % 2 else 0)  # odd problems: C only 8-byte aligned
+        storage = torch.full((lead + m * n + GUARD,), float("nan"), device="cuda", dtype=dtype)
+        ws.c[e] = storage[lead:lead + m * n].view(m, n)
+        ws.c_ptrs[e] = ws.c[e].data_ptr()
+        storages.append((storage, lead))
+    assert ws.homogeneous
+    code = _native.dtype_code(dtype)
+    assert _vector_layout(ws, code)
+    expected = [(a.double() @ b.double()).to(dtype) for a, b, _ in ws.problem_tensors()]
+    for bm, bn, bk, warps, stages in _tiles(dtype):
+        tiles = groups * -(-m // bm) * -(-n // bn)
+        for grid in sorted({1, 3, 8, 13, max(1, tiles // 3)}):
+            print(f"multi-tile homogeneous tile={(bm, bn, bk, warps, stages)} tiles={tiles} grid={grid}", flush=True)
+            for storage, _ in storages:
+                storage.fill_(float("nan"))
+            status = _native.library().moegemm_grouped_gemm(
+                ws.a_ptrs.data_ptr(), ws.b_ptrs.data_ptr(), ws.c_ptrs.data_ptr(), ws.dims.data_ptr(),
+                ws.strides.data_ptr(), groups, m, n, k, 1, tiles, code, 0, bm, bn, bk, 4, warps, stages, grid, 1,
+                _native.current_stream_handle(ws.a[0].device))
+            _native.check(status)
+            torch.cuda.synchronize()
+            for e, ((storage, lead), ref) in enumerate(zip(storages, expected)):
+                label = f"tile {(bm, bn, bk, warps, stages)} grid {grid} problem {e}"
+                assert torch.equal(ws.c[e], ref), label
+                assert torch.isnan(storage[:lead]).all() and torch.isnan(storage[lead + m * n:]).all(), label
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("pitch_pad", [8, 4], ids=["c16", "c8"])
+def test_single_every_tile_column_slice_small_grids(dtype, pitch_pad):
+    from kernels import _native
+
+    m, k, n = 333, 136, 520
+    pitch = n + pitch_pad
+    a, b = _ints((m, k), dtype), _ints((k, n), dtype)
+    expected = (a.double() @ b.double()).to(dtype)
+    wide = torch.empty((m + 2, pitch), device="cuda", dtype=dtype)
+    c = wide[1:m + 1, :n]  # rows 0 and m + 1 and the last pitch_pad columns are guards
+    code = _native.dtype_code(dtype)
+    for bm, bn, bk, warps, stages in _tiles(dtype):
+        tiles = -(-m // bm) * -(-n // bn)
+        for grid in sorted({1, 5, 16, max(1, tiles // 2)}):
+            print(f"multi-tile single tile={(bm, bn, bk, warps, stages)} pitch={pitch} tiles={tiles} grid={grid}",
+                  flush=True)
+            wide.fill_(float("nan"))
+            status = _native.library().moegemm_matmul(
+                a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, a.stride(0), a.stride(1), b.stride(0),
+                b.stride(1), c.stride(0), c.stride(1), code, 0, bm, bn, bk, 4, warps, stages, grid,
+                _native.current_stream_handle(a.device))
+            _native.check(status)
+            torch.cuda.synchronize()
+            label = f"tile {(bm, bn, bk, warps, stages)} grid {grid}"
+            assert torch.equal(c, expected), label
+            assert torch.isnan(wide[0]).all() and torch.isnan(wide[m + 1]).all(), label
+            assert torch.isnan(wide[:, n:]).all(), label
