@@ -80,6 +80,10 @@ def parser() -> argparse.ArgumentParser:
     p.add_argument("--heatmap-k", type=int, help="Defaults to model hidden_size")
     p.add_argument("--heatmap-ms", type=int_list)
     p.add_argument("--heatmap-ns", type=int_list)
+    p.add_argument("--heatmap-ks", type=int_list, help="K values of the heatmap (default: --heatmap-k alone)")
+    p.add_argument("--heatmap-gs", type=int_list,
+                   help="Group sizes G of the heatmap (default 1: the single GEMM); G > 1 runs G equal problems "
+                        "in one grouped launch")
     p.add_argument("--results-dir", type=Path, default=Path("results"))
     p.add_argument("--plots-dir", type=Path, default=Path("plots"))
     p.add_argument("--no-plots", action="store_true")
@@ -152,7 +156,7 @@ def main(argv: list[str] | None = None) -> int:
         raise ValueError("--peak-tflops must be positive")
     if args.input_precision == "tf32" and args.dtype != "fp32":
         raise ValueError("--input-precision tf32 requires --dtype fp32")
-    for name in ("moe_ms", "shape_ms", "heatmap_ms", "heatmap_ns"):
+    for name in ("moe_ms", "shape_ms", "heatmap_ms", "heatmap_ns", "heatmap_ks", "heatmap_gs"):
         values = getattr(args, name)
         if values is not None and (not values or any(v <= 0 for v in values)):
             raise ValueError(f"--{name.replace('_', '-')} must contain positive integers")

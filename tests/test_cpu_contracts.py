@@ -267,6 +267,42 @@ def test_moe_experiment_has_no_single_mode(tmp_path):
     assert set(calls) == {"grouped", "torch"}
 
 
+def test_heatmap_sweeps_group_sizes_and_k_values(tmp_path):
+    """G = 1 points take the single-GEMM path (the reference's heatmap); G > 1 points one grouped launch."""
+    from benchmark_shapes import run_heatmap
+
+    args = SimpleNamespace(heatmap_ms=[8, 128], heatmap_ns=[256], heatmap_k=7168, heatmap_ks=[256, 2880],
+                           heatmap_gs=[1, 8], results_dir=tmp_path)
+    single: list[tuple[int, int, int]] = []
+    grouped: list[tuple[int, int, int, int]] = []
+
+    def fake_single(_args, _env, m, k, n, experiment):
+        assert experiment == "heatmap"
+        single.append((m, k, n))
+        return [{"status": "skipped", "M": m, "K": k, "N": n}]
+
+    def fake_grouped(_args, _env, g, m, k, n):
+        grouped.append((g, m, k, n))
+        return [{"status": "skipped", "M": m, "K": k, "N": n, "num_gemms": g}]
+
+    with patch("benchmark_shapes._run_one", side_effect=fake_single), \
+            patch("benchmark_shapes._run_grouped_one", side_effect=fake_grouped), \
+            patch("benchmark_shapes.write_rows"):
+        rows = run_heatmap(args, {})
+    assert single == [(m, k, 256) for k in (256, 2880) for m in (8, 128)]
+    assert grouped == [(8, m, k, 256) for k in (256, 2880) for m in (8, 128)]
+    assert len(rows) == 8
+    # Without the new options the sweep is the reference's: G = 1 at --heatmap-k.
+    single.clear()
+    with patch("benchmark_shapes._run_one", side_effect=fake_single), patch("benchmark_shapes.write_rows"):
+        run_heatmap(SimpleNamespace(heatmap_ms=[8], heatmap_ns=[256], heatmap_k=4096, results_dir=tmp_path), {})
+    assert single == [(8, 4096, 256)]
+    for option in ("--heatmap-gs", "--heatmap-ks"):
+        assert getattr(parser().parse_args([option, "1,8"]), option[2:].replace("-", "_")) == [1, 8]
+        with pytest.raises(ValueError):
+            main([option, "0", "--no-plots"])
+
+
 def test_moe_sweep_argument_checks(tmp_path):
     base = dict(num_experts=8, parallel_size=4, ffn_size=16, hidden_size=32, topk=5, moe_ms=[3], tokens=None,
                 torch_baseline=False, results_dir=tmp_path)
