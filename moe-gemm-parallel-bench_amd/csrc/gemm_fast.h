@@ -310,8 +310,9 @@ struct FastTile {
                                                      int n0, int wave_m, int wave_n) {
     __shared__ int s_last;
     const int lane = threadIdx.x & 63;
-    float* tile_base = pd.partials + (int64_t)pd.tile * pd.splits * (BM * BN);
-    float* mine = tile_base + (int64_t)pd.split * (BM * BN);
+    // Partial slot of split sp: [tiles][splits][BM * BN].
+    auto slot = [&](int sp) -> float* { return pd.partials + ((int64_t)pd.tile * pd.splits + sp) * (BM * BN); };
+    float* mine = slot(pd.split);
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
       const int rl = wave_m * WTM + fm * MI + (lane % MI);
@@ -337,6 +338,31 @@ struct FastTile {
     __syncthreads();
     if (!s_last) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    // Sum the partials in split order, one whole partial tile at a time so that all of its loads
+    // are in flight together, into a register copy of the tile.
+    acc_t tot[FM][FN];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int i = 0; i < ACC; ++i) tot[fm][fn][i] = 0.0f;
+    for (int sp = 0; sp < pd.splits; ++sp) {
+      const float* src = slot(sp);
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+        const int rl = wave_m * WTM + fm * MI + (lane % MI);
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+          for (int q = 0; q < ACC / 4; ++q) {
+            const int cl = wave_n * WTN + fn * MI + ((MI == 32) ? (q * 8 + (lane >> 5) * 4) : ((lane >> 4) * 4));
+            const f32x4_t v = *MOEGEMM_GLOBAL(const f32x4_t, src + rl * BN + cl);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) tot[fm][fn][q * 4 + i] += v[i];
+          }
+      }
+    }
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
       const int rl = wave_m * WTM + fm * MI + (lane % MI);
@@ -349,9 +375,9 @@ struct FastTile {
         for (int q = 0; q < ACC / 4; ++q) {
           const int cl = wave_n * WTN + fn * MI + ((MI == 32) ? (q * 8 + (lane >> 5) * 4) : ((lane >> 4) * 4));
           if (n0 + cl >= pd.n) continue;
-          f32x4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
-          for (int sp = 0; sp < pd.splits; ++sp) sum += *MOEGEMM_GLOBAL(const f32x4_t, tile_base + sp * (BM * BN) + rl * BN + cl);
-          store4<E>(crow + (int64_t)(n0 + cl) * 2, sum);
+          const f32x4_t v = {tot[fm][fn][q * 4 + 0], tot[fm][fn][q * 4 + 1], tot[fm][fn][q * 4 + 2],
+                             tot[fm][fn][q * 4 + 3]};
+          store4<E>(crow + (int64_t)(n0 + cl) * 2, v);
         }
     }
   }

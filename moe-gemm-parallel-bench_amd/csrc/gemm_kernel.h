@@ -97,6 +97,7 @@ struct ProblemDesc {
   int32_t* counters;
 };
 
+
 // Wave-uniform copies: values derived from LDS (the generic-mode prefix search) are treated as
 // divergent by the compiler; reading lane 0 makes every descriptor scalar again, so table loads
 // become scalar loads and buffer resources need no waterfall loops.
@@ -648,6 +649,29 @@ struct TileQueue {
   }
 };
 
+// Problem and tile coordinates of tile t in a single or homogeneous launch (unsplit fields only).
+template <class T>
+__device__ __forceinline__ void simple_tile(const KParams& p, int t, ProblemDesc& pd, int& tm, int& tn) {
+  const int mt = (p.M + T::BM - 1) / T::BM, nt = (p.N + T::BN - 1) / T::BN;
+  if (p.mode == MODE_SINGLE) {
+    pd.a = static_cast<const char*>(p.a);
+    pd.b = static_cast<const char*>(p.b);
+    pd.c = static_cast<char*>(p.c);
+    pd.m = p.M; pd.n = p.N; pd.k = p.K;
+    pd.sam = p.sam; pd.sak = p.sak; pd.sbk = p.sbk; pd.sbn = p.sbn; pd.scm = p.scm; pd.scn = p.scn;
+    group_m_order(t, mt, nt, p.group_m, tm, tn);
+  } else {
+    const int per = mt * nt;
+    const int e = t / per;
+    group_m_order(t - e * per, mt, nt, p.group_m, tm, tn);
+    pd.a = reinterpret_cast<const char*>(p.a_ptrs[e]);
+    pd.b = reinterpret_cast<const char*>(p.b_ptrs[e]);
+    pd.c = reinterpret_cast<char*>(p.c_ptrs[e]);
+    pd.m = p.M; pd.n = p.N; pd.k = p.K;
+    pd.sam = p.K; pd.sak = 1; pd.sbk = p.N; pd.sbn = 1; pd.scm = p.swiglu ? p.N / 2 : p.N; pd.scn = 1;
+  }
+}
+
 template <class T>
 __global__ void __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WAVES_PER_EU)))
 grouped_gemm_kernel(KParams p) {
@@ -695,24 +719,8 @@ grouped_gemm_kernel(KParams p) {
     const int t = u % p.total_tiles;
     ProblemDesc pd;
     int tm, tn;
-    if (p.mode == MODE_SINGLE) {
-      pd.a = static_cast<const char*>(p.a);
-      pd.b = static_cast<const char*>(p.b);
-      pd.c = static_cast<char*>(p.c);
-      pd.m = p.M; pd.n = p.N; pd.k = p.K;
-      pd.sam = p.sam; pd.sak = p.sak; pd.sbk = p.sbk; pd.sbn = p.sbn; pd.scm = p.scm; pd.scn = p.scn;
-      const int mt = (p.M + T::BM - 1) / T::BM, nt = (p.N + T::BN - 1) / T::BN;
-      group_m_order(t, mt, nt, p.group_m, tm, tn);
-    } else if (p.mode == MODE_HOMOGENEOUS) {
-      const int mt = (p.M + T::BM - 1) / T::BM, nt = (p.N + T::BN - 1) / T::BN;
-      const int per = mt * nt;
-      const int e = t / per;
-      group_m_order(t - e * per, mt, nt, p.group_m, tm, tn);
-      pd.a = reinterpret_cast<const char*>(p.a_ptrs[e]);
-      pd.b = reinterpret_cast<const char*>(p.b_ptrs[e]);
-      pd.c = reinterpret_cast<char*>(p.c_ptrs[e]);
-      pd.m = p.M; pd.n = p.N; pd.k = p.K;
-      pd.sam = p.K; pd.sak = 1; pd.sbk = p.N; pd.sbn = 1; pd.scm = p.swiglu ? p.N / 2 : p.N; pd.scn = 1;
+    if (p.mode == MODE_SINGLE || p.mode == MODE_HOMOGENEOUS) {
+      simple_tile<T>(p, t, pd, tm, tn);
     } else {
       // A stolen unit may precede the loaded prefix chunk: restart from the first chunk.
       if (t < s_pref[0]) {

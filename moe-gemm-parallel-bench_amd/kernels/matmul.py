@@ -153,6 +153,17 @@ _PEAK_FLOPS_F32 = 1.573e14
 _HBM_BYTES_PER_S = 8.0e12
 
 
+def _mfma_fraction(cfg: KernelConfig) -> float:
+    """Sustained fraction of MFMA peak the model assumes for a tile config (measured ordering on
+    gfx950: the 8-wave 256 x 256 schedules lead; a wave tile past 128 x 64 accumulators spills)."""
+    wave_tile = (cfg.block_m * cfg.block_n) / max(1, cfg.num_warps)
+    if wave_tile > 8192:
+        return 0.3
+    if cfg.block_m == cfg.block_n == 256 and cfg.num_warps == 8:
+        return 0.85 if cfg.num_stages >= 3 else 0.8
+    return min(0.7, 0.25 + wave_tile / 16384.0)
+
+
 def estimate_seconds(
     shapes, cfg: KernelConfig, element_size: int, sm_count: int, f32: bool = False
 ) -> float:
@@ -176,8 +187,7 @@ def estimate_seconds(
     units = max(1, sm_count or 256)
     waves = math.ceil(tiles / units)
     quantisation = waves * units / tiles
-    wave_tile = (cfg.block_m * cfg.block_n) / max(1, cfg.num_warps)
-    mfma_fraction = min(0.85, 0.25 + wave_tile / 16384.0)
+    mfma_fraction = _mfma_fraction(cfg)
     peak = _PEAK_FLOPS_F32 if f32 else _PEAK_FLOPS_16BIT
     compute = padded / (peak * mfma_fraction) * quantisation
     # A tile's K loop streams at most ~1/units of HBM bandwidth; few tiles cannot use it all.
@@ -204,7 +214,7 @@ def matmul_candidate_configs(m: int, n: int, k: int, limit: int = 10, *, dtype=N
     ranked = sorted(
         family,
         key=lambda cfg: (estimate_seconds([(m, k, n)], cfg, element_size, sm_count, f32),
-                         -cfg.block_m * cfg.block_n, cfg.block_k, cfg.group_size_m),
+                         -_mfma_fraction(cfg), -cfg.block_m * cfg.block_n, cfg.block_k, cfg.group_size_m),
     )
     return tuple(diverse_configs(ranked, limit))
 
