@@ -304,7 +304,9 @@ struct FastTile {
     }
   }
 
-  __device__ static __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+  // silu(x) = x * sigmoid(x) = x / (1 + e^-x), with the hardware reciprocal (1 ulp) in place of an
+  // IEEE divide: the result is rounded to 16 bits, far coarser than either error.
+  __device__ static __forceinline__ float silu(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
   __device__ static __forceinline__ void split_store(const acc_t (&acc)[FM][FN], const ProblemDesc& pd, int m0,
                                                      int n0, int wave_m, int wave_n) {
