@@ -67,7 +67,7 @@ struct GemmTileEntry : GemmTile<E, BM, BN, BK, WM, WN> {};
 
 // 16-bit menu (bf16 and f16 share it): large-M MFMA-bound tiles down to skinny-M streaming tiles.
 // STAGES is sized to the 160 KiB LDS of a CU; the 2-stage narrow tiles at the end fit two
-// workgroups per CU (LDS, and registers via FastTile::WAVES_PER_EU), so one workgroup's prologue
+// workgroups per CU (LDS, and registers via FastTile::WAVES_PER_EU; 16x128 fits four), so one workgroup's prologue
 // overlaps the other's work on short-K groups.
 #define MOEGEMM_MENU_16BIT(X, E)                                                             \
   X(E, 256, 256, 64, 2, 4, 2) X(E, 256, 256, 64, 2, 2, 2) X(E, 256, 256, 32, 2, 2, 4)        \
@@ -78,7 +78,8 @@ struct GemmTileEntry : GemmTile<E, BM, BN, BK, WM, WN> {};
   X(E, 32, 256, 64, 1, 4, 4) X(E, 32, 128, 64, 1, 4, 4) X(E, 32, 128, 128, 1, 4, 3)          \
   X(E, 16, 256, 64, 1, 4, 4) X(E, 16, 256, 128, 1, 4, 2) X(E, 16, 128, 128, 1, 4, 4)         \
   X(E, 16, 64, 128, 1, 4, 4) X(E, 16, 64, 128, 1, 4, 7)                                    \
-  X(E, 16, 256, 64, 1, 4, 2) X(E, 32, 256, 64, 1, 4, 2) X(E, 64, 128, 64, 2, 2, 2)
+  X(E, 16, 256, 64, 1, 4, 2) X(E, 32, 256, 64, 1, 4, 2) X(E, 64, 128, 64, 2, 2, 2)        \
+  X(E, 16, 128, 64, 1, 4, 2)
 
 // fp32 menu (general kernel, v_mfma_f32_16x16x4_f32); STAGES is the register-staged double buffer.
 #define MOEGEMM_MENU_F32(X, E)                                                               \
