@@ -67,8 +67,8 @@ struct GemmTileEntry : GemmTile<E, BM, BN, BK, WM, WN> {};
 
 // 16-bit menu (bf16 and f16 share it): large-M MFMA-bound tiles down to skinny-M streaming tiles.
 // STAGES is sized to the 160 KiB LDS of a CU; the 2-stage narrow tiles at the end fit two
-// workgroups per CU (LDS, and registers via FastTile::WAVES_PER_EU; 16x128 fits four), so one workgroup's prologue
-// overlaps the other's work on short-K groups.
+// workgroups per CU (16x128 fits four; LDS, and registers via FastTile::WAVES_PER_EU), so one
+// workgroup's prologue overlaps another's work on short-K groups.
 #define MOEGEMM_MENU_16BIT(X, E)                                                             \
   X(E, 256, 256, 64, 2, 4, 2) X(E, 256, 256, 64, 2, 2, 2) X(E, 256, 256, 32, 2, 2, 4)        \
   X(E, 256, 256, 32, 2, 4, 4)                                                                \
