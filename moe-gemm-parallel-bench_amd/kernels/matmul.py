@@ -413,10 +413,14 @@ def _warm_clocks(launch, budget_ms: float = 100.0) -> None:
     torch.cuda.synchronize()
 
 
+_FINALISTS = 5
+
+
 def _tune(candidates, launch):
     """Hot-time every candidate (graph replays, bounded) after a clock warm-up, then re-time the best
-    three interleaved (three rounds of A, B, C) and keep the lowest median, so a clock drift during
-    tuning shifts every finalist alike instead of favouring whichever ran at the better moment."""
+    five interleaved (three rounds of A, B, C, D, E) and keep the lowest median, so a clock drift
+    during tuning shifts every finalist alike instead of favouring whichever ran at the better
+    moment, and a candidate that a noisy first pass ranked fourth or fifth still competes."""
     candidates = list(candidates)
     measured = []
     warmed = False
@@ -432,7 +436,7 @@ def _tune(candidates, launch):
     if not measured:
         raise RuntimeError("every autotune candidate failed to launch")
     measured.sort(key=lambda item: item[0])
-    finalists = [cfg for _, cfg in measured[:3]]
+    finalists = [cfg for _, cfg in measured[:_FINALISTS]]
     rounds: list[list[float]] = [[] for _ in finalists]
     for _ in range(3):
         for index, cfg in enumerate(finalists):
