@@ -159,6 +159,16 @@ def test_candidate_sets_are_bounded_unique_and_compiled():
                     assert KernelConfig(**{**cfg.as_dict(), "cta_multiplier": 1}) in _GROUPED_BASE_CONFIG_POOL
 
 
+def test_large_single_gemms_measure_the_eight_wave_256_tiles_first():
+    """The cost model ranks the 8-wave 256x256 schedules (ping-pong first) above the 4-wave
+    256x256 tiles, whose 128x128 wave tiles spill, so large single GEMMs always measure them."""
+    for m, n, k in ((2048, 7168, 7168), (2048, 7168, 2880), (1024, 28672, 4096), (8192, 8192, 8192),
+                    (2048, 7168, 256)):
+        keys = [cfg.tile_key for cfg in matmul_candidate_configs(m, n, k, dtype=torch.bfloat16, sm_count=256)]
+        assert keys[0] == (256, 256, 32, 8, 4), (m, n, k, keys)
+        assert (256, 256, 64, 4, 2) not in keys[:3] and (256, 256, 32, 4, 4) not in keys[:3]
+
+
 def test_grouped_candidates_cover_the_workload_families():
     skinny = grouped_candidate_configs(8, 4096, 7168, problem_count=32, sm_count=256)
     assert {c.block_m for c in skinny} <= {16, 32}
