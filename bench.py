@@ -14,8 +14,9 @@
   cases and the headline with the SwiGLU activation fused into the epilogue (a labelled variant:
   the reference times W13 without the activation), each timed the same way and checked against a
   float32 torch reference on a sample of experts.
-* ``cpu_baseline`` times the CPU oracle's blocked fp32-accumulating GEMM on the host cores on a
-  bounded sample of the same workload (rank 0, N = 1 only).
+* ``cpu_baseline`` times the reference's own CPU torch path for the headline step on the host cores
+  (per-expert ``torch.mm`` and ``F.grouped_mm`` over the padded offs layout; the faster is
+  reported, with core count and CPU model); ``cpu_oracle_port`` adds the oracle's C GEMM.
 """
 
 from __future__ import annotations
@@ -194,35 +195,93 @@ def _traffic_from_profiles(case: str):
     return float(match.group(1)) if match else None
 
 
-def _cpu_torch_mm(seconds_target: float = 5.0) -> dict:
-    """The reference's CPU path for this work, the per-expert torch.mm (benchmark_moe.py:258-266),
-    in bf16 on the host cores over a bounded sample of the same expert GEMM."""
+def _cpu_model() -> str:
+    """CPU model name of the host (lscpu's "Model name", from /proc/cpuinfo)."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_seconds(function, seconds_target: float, max_reps: int = 50) -> tuple[float, int]:
+    """1 untimed warm-up call, then timed calls until ``seconds_target`` (at least 3); median."""
+    function()
+    times = []
+    while len(times) < 3 or (sum(times) < seconds_target and len(times) < max_reps):
+        t0 = time.perf_counter()
+        function()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def _cpu_reference_path(seconds_per_method: float = 8.0) -> dict:
+    """The reference's CPU torch path on the host cores, over the headline step itself.
+
+    Step = the 32 DSV3 EP W13 expert products [512,7168]@[7168,4096] in bf16, timed two ways:
+      * the per-expert ``torch.mm`` loop of the reference's correctness reference
+        (benchmark_moe.py:258-266);
+      * one ``torch.nn.functional.grouped_mm`` over the expert-sorted 2-D A / 3-D B / int32 offs
+        layout with row strides padded to 16 bytes (kernels/torch_grouped_gemm.py:139-158, 162-174).
+    Each is a median over whole steps; the faster is ``value``, both are reported.
+    """
     import torch
+    import torch.nn.functional as F
 
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
+    experts, m, k, n = 32, 512, DSV3["hidden"], 2 * DSV3["ffn"]
     generator = torch.Generator().manual_seed(1234)
-    m, k, n = 512, DSV3["hidden"], 2 * DSV3["ffn"]
-    a = (torch.randn((m, k), generator=generator) * 0.1).to(torch.bfloat16)
-    b = (torch.randn((k, n), generator=generator) * 0.1).to(torch.bfloat16)
-    torch.mm(a, b[:, :256])  # warm
-    calls, elapsed = 0, 0.0
-    while elapsed < seconds_target and calls < 4096:
-        t0 = time.perf_counter()
-        torch.mm(a, b)
-        elapsed += time.perf_counter() - t0
-        calls += 1
+
+    def padded(columns: int) -> int:  # 16-byte row pitch for 2-byte elements
+        return -(-columns // 8) * 8
+
+    a_store = torch.empty((experts * m, padded(k)), dtype=torch.bfloat16)
+    b_store = torch.empty((experts, k, padded(n)), dtype=torch.bfloat16)
+    a_store.copy_(torch.randn(a_store.shape, generator=generator).mul_(0.1))
+    for index in range(experts):
+        b_store[index].copy_(torch.randn((k, padded(n)), generator=generator).mul_(0.1))
+    mat_a, mat_b = a_store[:, :k], b_store[:, :, :n]
+    offs = torch.arange(1, experts + 1, dtype=torch.int32) * m
+    flops = 2 * experts * m * k * n
+
+    def per_expert_loop():
+        for index in range(experts):
+            torch.mm(mat_a[index * m:(index + 1) * m], mat_b[index])
+
+    def grouped():
+        F.grouped_mm(mat_a, mat_b, offs=offs)
+
+    loop_s, loop_reps = _median_seconds(per_expert_loop, seconds_per_method)
+    rows = {"torch_mm_loop": {"value": flops / loop_s / 1e12, "reps": loop_reps, "seconds_per_step": loop_s}}
+    try:
+        grouped_s, grouped_reps = _median_seconds(grouped, seconds_per_method)
+        rows["torch_grouped_mm"] = {"value": flops / grouped_s / 1e12, "reps": grouped_reps,
+                                    "seconds_per_step": grouped_s}
+    except RuntimeError as exc:  # a torch without a CPU grouped_mm kernel for this layout
+        rows["torch_grouped_mm"] = {"value": None, "error": str(exc)[:200]}
+    best = max((r for r in rows.values() if r.get("value")), key=lambda r: r["value"])
+    best_name = next(name for name, r in rows.items() if r is best)
     return {
-        "value": calls * 2 * m * k * n / elapsed / 1e12,
+        "value": best["value"],
         "unit": "TFLOP/s",
         "cores": threads,
-        "kind": "reference-path torch.mm",
-        "sample": f"{calls} calls of one expert's [512,7168]@[7168,4096] bf16 torch.mm ({elapsed:.1f} s)",
+        "kind": "reference",
+        "cpu_model": _cpu_model(),
+        "method": best_name,
+        "methods": rows,
+        "sample": f"the whole headline step (32 x [512,7168]@[7168,4096] bf16, {flops / 1e9:.1f} GFLOP) per "
+                  f"timed call, median of >=3 calls (~{seconds_per_method:.0f} s per method); the reference's "
+                  "own CPU torch computation (per-expert torch.mm and F.grouped_mm on the 16-byte padded "
+                  "2-D/3-D + offs layout), torch.set_num_threads(cores)",
     }
 
 
-def _cpu_baseline(seconds_target: float = 12.0) -> dict:
-    """Oracle blocked GEMM on the host cores over a bounded sample of the workload."""
+def _cpu_oracle_port(seconds_target: float = 5.0) -> dict:
+    """Extra: the oracle's blocked OpenMP fp32-accumulating C GEMM on the same host cores."""
     import numpy as np
 
     from oracle import oracle
@@ -232,27 +291,22 @@ def _cpu_baseline(seconds_target: float = 12.0) -> dict:
     rng = np.random.default_rng(1234)
 
     def bf16(shape):
-        return (rng.standard_normal(shape, dtype=np.float32) * 0.1).view(np.uint32).__rshift__(16).astype(np.uint16)
+        return oracle.to_bf16_bits(rng.standard_normal(shape, dtype=np.float32) * 0.1)
 
     a = bf16((m, k))
-    b = bf16((k, n))
-    # Sample: whole [512, 7168] @ [7168, cols] expert slices, growing until ~seconds_target.
     cols = 256
-    oracle.gemm_fast_bf16(a[:16], b[:, :cols], threads)  # warm (thread pool, pages)
+    b = bf16((k, cols))
+    oracle.gemm_fast_bf16(a[:16], b, threads)  # warm (thread pool, pages)
     done_flops, elapsed, slices = 0, 0.0, 0
     while elapsed < seconds_target and slices < 4096:
         t0 = time.perf_counter()
-        oracle.gemm_fast_bf16(a, np.ascontiguousarray(b[:, (slices * cols) % n:(slices * cols) % n + cols]), threads)
+        oracle.gemm_fast_bf16(a, b, threads)
         elapsed += time.perf_counter() - t0
         done_flops += 2 * m * k * cols
         slices += 1
     return {
-        "value": done_flops / elapsed / 1e12,
-        "unit": "TFLOP/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": f"{slices} slices of one expert's [512,7168]@[7168,{cols}] bf16 GEMM "
-                  f"({done_flops / 1e9:.1f} GFLOP, {elapsed:.1f} s), oracle blocked fp32-accumulating C GEMM",
+        "value": done_flops / elapsed / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+        "sample": f"{slices} x [512,7168]@[7168,{cols}] bf16 slices ({elapsed:.1f} s)",
     }
 
 
@@ -352,8 +406,8 @@ def main(argv=None) -> int:
         "cases": cases,
     }
     if not args.no_cpu:
-        line["cpu_baseline"] = _cpu_baseline()
-        line["cpu_torch_mm"] = _cpu_torch_mm()
+        line["cpu_baseline"] = _cpu_reference_path()
+        line["cpu_oracle_port"] = _cpu_oracle_port()
     print(json.dumps(line))
     return 0 if headline["correct"] and all(c["correct"] for c in cases) else 1
 

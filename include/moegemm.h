@@ -47,7 +47,7 @@ const char* moegemm_last_error(void);
 
 /*
  * Compiled tile configurations.  Replaces the Triton config pools
- * (reference kernels/matmul.py:95-139 _MATMUL_CONFIG_POOL and kernels/grouped_gemm.py:41-64
+ * (reference kernels/matmul.py:54-98 _MATMUL_CONFIG_POOL and kernels/grouped_gemm.py:41-64
  * _GROUPED_EXTRA_CONFIG_POOL): the Python candidate generators enumerate this table instead.
  * moegemm_kernel_info fills out7 = {block_m, block_n, block_k, num_warps (wave64 per
  * workgroup), num_stages (LDS stages), lds_bytes, waves_m}.
@@ -121,7 +121,7 @@ int moegemm_grouped_gemm_swiglu(const int64_t* a_ptrs, const int64_t* b_ptrs, co
 
 /*
  * Split-K in one launch, for problems with fewer output tiles than CUs (the reference's G = 1
- * Mixtral EP path, kernels/grouped_gemm.py:629-640 -> kernels/matmul.py:373-433, runs one
+ * Mixtral EP path, kernels/grouped_gemm.py:629-640 -> kernels/matmul.py:332-392, runs one
  * workgroup per tile and leaves most of the GPU idle on a skinny-N, long-K W2).  Each output tile
  * is computed by `splits` units over K ranges of whole block_k slices; each unit writes its fp32
  * partial tile into `workspace`, and the last unit of a tile (counted with one atomic per unit)
@@ -206,8 +206,8 @@ int moegemm_grouped_mm_offs_stealing(const void* a, const void* b, void* c, cons
 
 /*
  * Masked single GEMM with arbitrary strides, C = A @ B.  Replaces the Triton launch of
- * reference kernels/matmul.py:373-433 (launch_matmul -> _matmul_kernel_impl, :264-314); shape
- * and dtype validation (kernels/matmul.py:359-370) stays in Python.  grid_size <= 0 launches one
+ * reference kernels/matmul.py:332-392 (launch_matmul -> _matmul_kernel_impl, :223-273); shape
+ * and dtype validation (_validate_matrices, kernels/matmul.py:318-329) stays in Python.  grid_size <= 0 launches one
  * workgroup per output tile like the reference's 1-D grid; a positive value makes it persistent.
  * The LDS-DMA kernel is chosen automatically when the operands meet its layout preconditions.
  */

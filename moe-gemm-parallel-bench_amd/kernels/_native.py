@@ -3,7 +3,7 @@
 The library is built in-tree next to this file (``csrc/Makefile`` or ``__graft_entry__.build()``).
 Nothing here falls back to another implementation: when the library or a GPU is missing, every
 launch raises ``RuntimeError``, mirroring the reference's "Triton with an active CUDA driver is
-required" error (reference kernels/grouped_gemm.py:626-627, kernels/matmul.py:383-384).
+required" error (reference kernels/grouped_gemm.py:626-627, kernels/matmul.py:342-343).
 """
 
 from __future__ import annotations

@@ -55,6 +55,10 @@ def _validate(mat_a, mat_b, offs, out):
         raise ValueError(f"contraction mismatch: mat_a K={k}, mat_b K={kb}")
     if offs.ndim != 1 or offs.dtype != torch.int32 or offs.shape[0] != groups:
         raise ValueError(f"offs must be an int32 vector with one entry per group ({groups})")
+    if not offs.is_contiguous():
+        # The kernel reads offs[e] as a dense int32 array from its base address: a strided view
+        # would give wrong group boundaries and an expanded one would read past its storage.
+        raise ValueError("offs must be contiguous (pass offs.contiguous())")
     if groups <= 0 or k <= 0 or n <= 0:
         raise ValueError("grouped_mm needs at least one group and positive K and N")
     devices = {mat_a.device, mat_b.device, offs.device}

@@ -1,14 +1,14 @@
 """Masked single GEMM on gfx950: config record, compiled tile menu, candidates and launcher.
 
 Public surface and behaviour follow the reference's kernels/matmul.py:
-  * ``KernelConfig`` (reference :60-73) with the same fields.  On this backend ``num_warps`` is the
+  * ``KernelConfig`` (reference :19-32) with the same fields.  On this backend ``num_warps`` is the
     number of wave64 wavefronts per workgroup and ``num_stages`` the number of LDS stages of the
     K pipeline; ``group_size_m`` is the GROUP_M traversal width and ``cta_multiplier`` the
     persistent-grid multiplier of grouped launches.
-  * ``select_config`` (:76-86) is the heuristic fallback; ``matmul_candidate_configs`` (:187-211)
-    returns a bounded shape-family candidate set; ``diverse_configs`` (:142-161) keeps coverage of
+  * ``select_config`` (:35-45) is the heuristic fallback; ``matmul_candidate_configs`` (:146-170)
+    returns a bounded shape-family candidate set; ``diverse_configs`` (:101-120) keeps coverage of
     tile/traversal choices when truncating a ranked list.
-  * ``launch_matmul`` (:373-433) validates like ``_validate_matrices`` (:359-370): ValueError for
+  * ``launch_matmul`` (:332-392) validates like ``_validate_matrices`` (:318-329): ValueError for
     bad shapes/dtypes/devices, RuntimeError when the native library or a GPU is missing.  With
     ``autotune=True`` the first call for a shape key measures the candidates (hot graph timing)
     and later calls are a cache lookup plus exactly one kernel launch (capturable).

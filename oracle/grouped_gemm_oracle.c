@@ -10,9 +10,10 @@
  *     dims[e] = (m, n, k) (order built at :536) and strides[e] = (am, ak, bk, bn, cm, cn)
  *     (order built at :537-544), C_e[i, j] = sum_l A_e[i, l] * B_e[l, j];
  *   - kernels/grouped_gemm.py:321-397 (homogeneous) is the same sum with contiguous strides;
- *   - kernels/matmul.py:264-314: fp32 accumulator (:297), result cast to C's dtype on store
- *     (:310-314), masked tails contribute nothing;
- *   - input_precision "tf32" (kernels/matmul.py:309) rounds fp32 operands to a 10-bit mantissa.
+ *   - kernels/matmul.py:223-273 (_matmul_kernel_impl): fp32 accumulator (:256), result cast to
+ *     C's dtype on store (:269-273), masked tails contribute nothing (:258-267);
+ *   - input_precision "tf32" (the tl.dot argument, kernels/matmul.py:268) rounds fp32 operands to
+ *     a 10-bit mantissa.
  * Products of two fp16/bf16 values are exact in fp32; the sum is accumulated in double
  * (accum = ORACLE_ACCUM_F64, the tight reference) or sequentially in float
  * (ORACLE_ACCUM_F32, the reference's fp32-accumulated model), then rounded to nearest-even.
@@ -152,8 +153,9 @@ int oracle_grouped_gemm(int32_t problem_count, const void* const* a_ptrs, const 
 }
 
 /*
- * Fast contiguous fp32-accumulating variant for timing the CPU baseline: C = A @ B with A [m,k],
- * B [k,n] row-major 16-bit operands.  Work is split into (16-row x 256-column) blocks over
+ * Fast contiguous fp32-accumulating variant, kept as an extra CPU timing: C = A @ B with A [m,k],
+ * B [k,n] row-major 16-bit operands.  Each output is the float32 running sum over k in index
+ * order, so it is bit-equal to oracle_gemm with ORACLE_ACCUM_F32 (pinned in tests/test_oracle.py).  Work is split into (16-row x 256-column) blocks over
  * OpenMP threads; each block keeps its fp32 accumulators in L1 and streams the matching B
  * column panel once per block, converting 16-bit values as it goes.  scratch_rows is unused
  * (kept for ABI stability of the test binding).

@@ -6,7 +6,7 @@ launch rules.  Only tests/, ``__graft_entry__.smoke()`` and bench.py's ``cpu_bas
 import this module, and only as the checker; the product path never does.
 
 Functions and the reference code they restate:
-  * ``gemm`` / ``grouped_gemm``     kernels/grouped_gemm.py:399-482 and kernels/matmul.py:264-314
+  * ``gemm`` / ``grouped_gemm``     kernels/grouped_gemm.py:399-482 and kernels/matmul.py:223-273
                                     (fp32-exact products, fp32/fp64 accumulation, cast on store);
                                     pinned by tests/test_oracle.py against the golden fixtures
                                     (torch CPU float64), closed forms, brute force and numpy.
@@ -14,7 +14,7 @@ Functions and the reference code they restate:
                                     strides (am, ak, bk, bn, cm, cn)); pinned by brute force.
   * ``is_homogeneous``              kernels/grouped_gemm.py:550-552; pinned by reference tests'
                                     expectations (tests/test_gpu.py:99-125 of the reference).
-  * ``dispatch``                    kernels/grouped_gemm.py:629-640, 652, 712 (scheduler names).
+  * ``dispatch``                    kernels/grouped_gemm.py:629-640, 682, 709, 739, 760 (scheduler names).
   * ``grid_size``                   kernels/grouped_gemm.py:597-599.
   * ``tile_order``                  kernels/grouped_gemm.py:353-360 (GROUP_M traversal + persistent
                                     stride); pinned by a coverage/bijection check.
@@ -32,6 +32,11 @@ Functions and the reference code they restate:
   * ``offsets_tile_bound``          the host's tile-count bound for that layout (each group adds at
                                     most one partial M tile); pinned by exhaustive small cases.
   * ``to_bf16_bits`` / ``to_f16_bits``  round-to-nearest-even casts; pinned against torch/numpy.
+  * ``gemm_fast_bf16``              the same fp32 running sum as ``gemm(accum="f32")``, blocked and
+                                    threaded (an extra CPU timing in bench.py); pinned bit for bit
+                                    against a numpy float32 running sum with torch's cast, against
+                                    ``gemm(accum="f32")``, within the float32 accumulation bound of
+                                    the golden sums, and by a planted dropped term.
 """
 
 from __future__ import annotations

@@ -453,6 +453,22 @@ def test_grouped_mm_validates_before_touching_a_gpu():
         grouped_mm(a, b[:, :8], offs)
 
 
+def test_grouped_mm_rejects_strided_and_expanded_offs():
+    """The kernel reads offs as a dense int32 array: a strided view would give wrong group
+    boundaries and an expanded (stride 0) one would read past its storage."""
+    from kernels.grouped_mm import grouped_mm, grouped_mm_swiglu
+
+    a = torch.zeros((8, 16), dtype=torch.bfloat16)
+    b = torch.zeros((2, 16, 32), dtype=torch.bfloat16)
+    strided = torch.tensor([[4, 0], [8, 0]], dtype=torch.int32)[:, 0]
+    expanded = torch.tensor([8], dtype=torch.int32).expand(2)
+    for offs in (strided, expanded):
+        assert not offs.is_contiguous()
+        for launch in (grouped_mm, grouped_mm_swiglu):
+            with pytest.raises(ValueError, match="contiguous"):
+                launch(a, b, offs)
+
+
 def test_grouped_mm_swiglu_validates_before_touching_a_gpu():
     from kernels.grouped_mm import grouped_mm_swiglu
 

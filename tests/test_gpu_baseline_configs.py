@@ -107,28 +107,6 @@ def test_heatmap_tail_shapes_against_oracle():
             assert normwise(c, oracle_product(a, b)) <= 1e-2
 
 
-HEATMAP_GRID = [(g, m, n, k) for g in (1, 8) for m in (8, 128, 2048) for n in (256, 2880, 7168) for k in (256, 2880)]
-
-
-@pytest.mark.parametrize("point", HEATMAP_GRID, ids=lambda p: "g{}_m{}_n{}_k{}".format(*p))
-def test_heatmap_grid_heuristic_config_against_float32_torch(point):
-    """BASELINE heatmap family (bf16, non-multiple extents such as 2880), heuristic config and
-    heuristic split, first and last problem against a float32 torch product."""
-    from kernels.grouped_gemm import build_grouped_workspace, launch_grouped
-
-    g, m, n, k = point
-    print(f"heatmap grid G={g} M={m} N={n} K={k}", flush=True)
-    workspace = build_grouped_workspace([(m, k, n)] * g, torch.bfloat16, seed=m + n + k)
-    for c in workspace.c:
-        c.fill_(float("nan"))
-    launch_grouped(workspace, autotune=False)
-    torch.cuda.synchronize()
-    for index in sorted({0, g - 1}):
-        a, b, c = workspace.a[index], workspace.b[index], workspace.c[index]
-        assert torch.isfinite(c).all(), f"problem {index} left unwritten with {workspace.config}"
-        assert normwise(c, a.float() @ b.float()) <= 1e-2, f"problem {index} with {workspace.config}"
-
-
 def test_graph_timing_excludes_host_delay_and_visits_cold_ring():
     from utils.benchmark import time_cuda
 

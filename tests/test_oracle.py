@@ -316,3 +316,65 @@ def test_swiglu_reference_matches_torch_float64(dtype):
     assert not np.allclose(swapped, theirs, rtol=1e-2, atol=1e-3)  # planted: gate and up exchanged
     with pytest.raises(ValueError):
         oracle.swiglu_reference(a, b[:, :-1], dtype)
+
+
+# ---------------------------------------------------------------------------------------------
+# The OpenMP fp32-accumulating GEMM (``gemm_fast_bf16``), used only to time a CPU baseline.
+
+def _sequential_f32_reference(a_bits: np.ndarray, b_bits: np.ndarray, dtype: str) -> np.ndarray:
+    """numpy float32 running sum over k in index order (each 16-bit product is exact in float32),
+    rounded to the 16-bit dtype by torch's cast: an implementation independent of the C oracle."""
+    import torch
+
+    a = _values(a_bits, dtype).astype(np.float32)
+    b = _values(b_bits, dtype).astype(np.float32)
+    acc = np.zeros((a.shape[0], b.shape[1]), dtype=np.float32)
+    for index in range(a.shape[1]):
+        acc = acc + a[:, index:index + 1] * b[index:index + 1, :]
+    torch_dtype = torch.bfloat16 if dtype == "bf16" else torch.float16
+    return torch.from_numpy(acc).to(torch_dtype).view(torch.int16).numpy().view(np.uint16)
+
+
+_FAST_SHAPES = [(1, 5, 3), (17, 13, 31), (33, 70, 65), (19, 200, 300), (40, 256, 320), (3, 1000, 257)]
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("shape", _FAST_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_fast_gemm_is_bit_equal_to_sequential_f32_sums(dtype, shape):
+    """Ragged m and n (not multiples of the 16 x 256 blocks) and K not a multiple of 16."""
+    m, k, n = shape
+    rng = np.random.default_rng(m * 1000 + k + n)
+    to_bits = oracle.to_bf16_bits if dtype == "bf16" else oracle.to_f16_bits
+    a = to_bits(rng.standard_normal((m, k)).astype(np.float32) / math.sqrt(k))
+    b = to_bits(rng.standard_normal((k, n)).astype(np.float32))
+    fast = oracle.gemm_fast_bf16(a, b, 4, dtype)
+    np.testing.assert_array_equal(fast, _sequential_f32_reference(a, b, dtype))
+    np.testing.assert_array_equal(fast, oracle.gemm(a, b, dtype, accum="f32"))
+
+
+@pytest.mark.parametrize("name", [n for n in map(str, GOLDEN["case_names"]) if not n.startswith("fp32")])
+def test_fast_gemm_within_f32_accumulation_bound_of_golden(name):
+    """Against the torch float64 golden sums: the difference is at most the float32 running-sum
+    error k * 2^-24 * sum|a||b| plus one output rounding of the 16-bit dtype."""
+    dtype = name.split("_")[0]
+    a, b = GOLDEN[f"{name}_a"], GOLDEN[f"{name}_b"]
+    exact = GOLDEN[f"{name}_exact"]
+    fast = _values(oracle.gemm_fast_bf16(a, b, 2, dtype), dtype)
+    k = a.shape[1]
+    magnitude = np.abs(_values(a, dtype)) @ np.abs(_values(b, dtype))
+    unit = 2.0**-8 if dtype == "bf16" else 2.0**-11
+    bound = k * 2.0**-24 * magnitude + unit * np.abs(exact) + 1e-30
+    assert np.all(np.abs(fast - exact) <= bound)
+    # Rounded outputs agree with the golden ones except where the f32 sum crosses a rounding edge.
+    assert np.mean(oracle.gemm_fast_bf16(a, b, 2, dtype) == GOLDEN[f"{name}_out"]) > 0.9
+
+
+def test_fast_gemm_planted_dropped_term_fails():
+    m, k, n = 16, 64, 128
+    rng = np.random.default_rng(5)
+    a = oracle.to_bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
+    b = oracle.to_bf16_bits(rng.standard_normal((k, n)).astype(np.float32))
+    fast = oracle.gemm_fast_bf16(a, b, 2)
+    dropped = oracle.gemm_fast_bf16(np.ascontiguousarray(a[:, 1:]), np.ascontiguousarray(b[1:]), 2)
+    assert not np.array_equal(fast, dropped)
+    assert not np.array_equal(dropped, _sequential_f32_reference(a, b, "bf16"))
