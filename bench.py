@@ -229,31 +229,22 @@ def _cpu_reference_path(seconds_per_method: float = 8.0) -> dict:
     Each is a median over whole steps; the faster is ``value``, both are reported.
     """
     import torch
-    import torch.nn.functional as F
+
+    from kernels.torch_grouped_gemm import build_torch_grouped_workspace, launch_torch_grouped
 
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
     experts, m, k, n = 32, 512, DSV3["hidden"], 2 * DSV3["ffn"]
-    generator = torch.Generator().manual_seed(1234)
-
-    def padded(columns: int) -> int:  # 16-byte row pitch for 2-byte elements
-        return -(-columns // 8) * 8
-
-    a_store = torch.empty((experts * m, padded(k)), dtype=torch.bfloat16)
-    b_store = torch.empty((experts, k, padded(n)), dtype=torch.bfloat16)
-    a_store.copy_(torch.randn(a_store.shape, generator=generator).mul_(0.1))
-    for index in range(experts):
-        b_store[index].copy_(torch.randn((k, padded(n)), generator=generator).mul_(0.1))
-    mat_a, mat_b = a_store[:, :k], b_store[:, :, :n]
-    offs = torch.arange(1, experts + 1, dtype=torch.int32) * m
+    # The torch provider's own layout builder, on the host: padded 2-D A / 3-D B / int32 offs.
+    workspace = build_torch_grouped_workspace([(m, k, n)] * experts, torch.bfloat16, seed=1234, device="cpu")
     flops = 2 * experts * m * k * n
 
     def per_expert_loop():
         for index in range(experts):
-            torch.mm(mat_a[index * m:(index + 1) * m], mat_b[index])
+            torch.mm(workspace.mat_a[index * m:(index + 1) * m], workspace.mat_b[index])
 
     def grouped():
-        F.grouped_mm(mat_a, mat_b, offs=offs)
+        launch_torch_grouped(workspace)
 
     loop_s, loop_reps = _median_seconds(per_expert_loop, seconds_per_method)
     rows = {"torch_mm_loop": {"value": flops / loop_s / 1e12, "reps": loop_reps, "seconds_per_step": loop_s}}
@@ -261,7 +252,7 @@ def _cpu_reference_path(seconds_per_method: float = 8.0) -> dict:
         grouped_s, grouped_reps = _median_seconds(grouped, seconds_per_method)
         rows["torch_grouped_mm"] = {"value": flops / grouped_s / 1e12, "reps": grouped_reps,
                                     "seconds_per_step": grouped_s}
-    except RuntimeError as exc:  # a torch without a CPU grouped_mm kernel for this layout
+    except RuntimeError as exc:  # a torch without a CPU grouped_mm kernel for this layout (incl. unavailable)
         rows["torch_grouped_mm"] = {"value": None, "error": str(exc)[:200]}
     best = max((r for r in rows.values() if r.get("value")), key=lambda r: r["value"])
     best_name = next(name for name, r in rows.items() if r is best)

@@ -1,17 +1,16 @@
-"""Device timing, tuning, dtype, memory and correctness helpers (HIP/ROCm).
+"""Device timing, tuning, dtype, memory and correctness helpers on ROCm.
 
-Same public names and semantics as the reference's utils/benchmark.py:
-  * ``time_cuda`` (reference utils/benchmark.py:154-198) times device execution from graph
-    replays, so host dispatch never lands inside a sample.  The reference captures one event pair
-    per call inside the graph; ROCm torch forbids external events in a capture, so here each
-    sample is one timed replay of a chunk of whole rings (mean per-call time of that replay).
-    Warmup and repeat counts are capped towards a 250 ms warmup and ``target_ms`` measurement
-    budget, then rounded up to whole workspace rings, as in the reference.
-  * ``tune_rotating_configs`` (:201-246) picks a fixed config by timing each candidate across the
-    whole rotating ring; candidates that raise ``RuntimeError``/``AssertionError`` are discarded.
-  * ``hot_autotune_bench`` (:249-258) is the bounded hot timer used by the launchers' autotuner.
-  * ``assert_close`` (:261-271) applies the per-dtype tolerances and reports max abs/rel error.
-On ROCm the graph is a hipGraph.
+These names form the helper surface that the reference's drivers import from utils/benchmark.py
+(reference utils/benchmark.py:13-278): the timing record, the graph timer, the rotating-ring
+tuner, the hot timer behind the launchers' autotuner, dtype/device helpers, the memory budget and
+the per-dtype closeness check.  The implementations are this project's own:
+  * ``time_cuda`` measures device time from hipGraph replays of chunks of whole workspace rings
+    (ROCm torch refuses external events inside a capture, so the reference's per-call event
+    nodes are not available); counts are capped towards a 250 ms warm-up and ``target_ms`` of
+    measurement and rounded up to whole rings;
+  * ``tune_rotating_configs`` times every candidate across the complete rotating ring and keeps
+    the lowest median; a candidate that cannot launch is counted as failed and skipped;
+  * ``assert_close`` applies the reference's per-dtype (rtol, atol) and reports max abs / rel.
 """
 
 from __future__ import annotations
@@ -22,11 +21,20 @@ from collections.abc import Callable, Sequence
 from dataclasses import dataclass
 from typing import TypeVar
 
+import numpy as np
+
 TIMING_METHOD = "hip_graph_replay_events"
 ConfigT = TypeVar("ConfigT")
 
-# Per-dtype assert_close tolerances (rtol, atol), as the reference's utils/benchmark.py:268.
-TOLERANCES = {"fp16": (2e-2, 2e-2), "bf16": (5e-2, 5e-2), "fp32": (2e-3, 2e-3)}
+# name -> (torch dtype attribute, bytes per element, (rtol, atol) of assert_close).  The
+# tolerances are the reference's result contract (utils/benchmark.py:268).
+_DTYPE_TABLE = {
+    "fp16": ("float16", 2, (2e-2, 2e-2)),
+    "bf16": ("bfloat16", 2, (5e-2, 5e-2)),
+    "fp32": ("float32", 4, (2e-3, 2e-3)),
+}
+TOLERANCES = {name: entry[2] for name, entry in _DTYPE_TABLE.items()}
+_HEADROOM_BYTES = 256 << 20
 
 
 @dataclass(frozen=True)
@@ -48,79 +56,79 @@ class TuningResult:
     candidates_failed: int
 
 
+def _dtype_entry(name: str):
+    try:
+        return _DTYPE_TABLE[name]
+    except KeyError:
+        raise ValueError(f"unknown dtype name {name!r}; expected one of {sorted(_DTYPE_TABLE)}") from None
+
+
 def torch_dtype(name: str):
     import torch
 
-    table = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}
-    if name not in table:
-        raise ValueError(f"unknown dtype name {name!r}")
-    return table[name]
+    return getattr(torch, _dtype_entry(name)[0])
 
 
 def dtype_size(name: str) -> int:
-    return {"fp16": 2, "bf16": 2, "fp32": 4}[name]
+    return _dtype_entry(name)[1]
 
 
 def select_cuda_device(device_spec: str) -> str:
-    """Select one logical GPU (``cuda`` / ``cuda:N``; HIP_VISIBLE_DEVICES is honoured by torch)."""
+    """Make one logical GPU current and return it as ``cuda:N``.
+
+    ROCm torch names HIP devices ``cuda``; the index is logical within HIP_VISIBLE_DEVICES /
+    ROCR_VISIBLE_DEVICES, exactly as torch enumerates them.
+    """
+    kind, _, index_text = device_spec.partition(":")
+    if kind != "cuda" or (index_text and not index_text.isdigit()):
+        raise ValueError("--device must name a GPU device (for example cuda or cuda:1)")
     try:
         import torch
     except ImportError:
-        if device_spec == "cuda" or device_spec.startswith("cuda:"):
-            return device_spec
-        raise ValueError("--device must name a GPU device (for example cuda or cuda:1)")
-    device = torch.device(device_spec)
-    if device.type != "cuda":
-        raise ValueError("--device must name a GPU device (for example cuda or cuda:1)")
+        return device_spec
     if not torch.cuda.is_available():
         return device_spec
-    index = torch.cuda.current_device() if device.index is None else device.index
-    count = torch.cuda.device_count()
-    if not 0 <= index < count:
-        raise ValueError(f"--device selects logical GPU {index}, but only {count} device(s) are visible")
+    visible = torch.cuda.device_count()
+    index = int(index_text) if index_text else torch.cuda.current_device()
+    if index >= visible:
+        raise ValueError(f"--device selects logical GPU {index}, but only {visible} device(s) are visible")
     torch.cuda.set_device(index)
     return f"cuda:{index}"
 
 
 def configure_torch_matmul(input_precision: str) -> None:
-    """Align torch's fp32 matmul policy with the kernels' ``input_precision``."""
+    """Give torch's fp32 matmuls (the correctness references) the kernels' input precision."""
     try:
         import torch
     except ImportError:
         return
-    tf32 = input_precision == "tf32"
-    torch.backends.cuda.matmul.allow_tf32 = tf32
-    torch.set_float32_matmul_precision("high" if tf32 else "highest")
+    if input_precision not in ("ieee", "tf32"):
+        raise ValueError(f"input_precision must be 'ieee' or 'tf32', got {input_precision!r}")
+    torch.backends.cuda.matmul.allow_tf32 = input_precision == "tf32"
+    torch.set_float32_matmul_precision({"ieee": "highest", "tf32": "high"}[input_precision])
 
 
 def dtype_supported(name: str) -> tuple[bool, str]:
-    """Probe a dtype with a real device matmul."""
+    """(supported, reason): run a small device matmul in the dtype and check it is finite."""
     try:
         import torch
-
-        if not torch.cuda.is_available():
-            return False, "GPU unavailable"
-        x = torch.ones((16, 16), device="cuda", dtype=torch_dtype(name))
-        y = torch.mm(x, x)
-        torch.cuda.synchronize()
-        if not bool(torch.isfinite(y).all().item()):
-            return False, f"{name} device matmul produced non-finite output"
-        return True, ""
-    except Exception as exc:  # pragma: no cover - exercised only on broken stacks
+    except ImportError:
+        return False, "PyTorch unavailable"
+    if not torch.cuda.is_available():
+        return False, "GPU unavailable"
+    try:
+        probe = torch.full((16, 16), 0.5, device="cuda", dtype=torch_dtype(name))
+        finite = bool(torch.isfinite(probe @ probe).all().item())
+    except Exception as exc:  # noqa: BLE001 - any failure means "not usable"
         return False, f"{name} device matmul probe failed: {exc!r}"
+    return (True, "") if finite else (False, f"{name} device matmul produced non-finite output")
 
 
 def percentile(values: Sequence[float], q: float) -> float:
-    """Linear-interpolated percentile, q in [0, 1]."""
-    ordered = sorted(values)
-    if not ordered:
+    """Linear-interpolation percentile for q in [0, 1] (numpy's default method); NaN when empty."""
+    if len(values) == 0:
         return math.nan
-    position = (len(ordered) - 1) * q
-    low = math.floor(position)
-    high = math.ceil(position)
-    if low == high:
-        return ordered[low]
-    return ordered[low] + (ordered[high] - ordered[low]) * (position - low)
+    return float(np.percentile(np.asarray(values, dtype=np.float64), 100.0 * q))
 
 
 def _whole_ring_count(requested: int, minimum: int, workspace_count: int) -> int:
@@ -227,7 +235,14 @@ def tune_rotating_configs(
     workspace_count: int,
     repeats_per_workspace: int = 2,
 ) -> TuningResult:
-    """Pick the fastest fixed config while rotating through every resident workspace."""
+    """Choose one fixed config by timing each candidate across the whole rotating ring.
+
+    Each candidate gets the same graph timing as the measurement itself (``time_cuda`` over
+    ``workspace_count`` buffers, at least three and ``repeats_per_workspace`` visits per buffer),
+    so the choice reflects the cold-ring access pattern.  Candidates whose launch raises
+    (``RuntimeError``, ``ValueError`` for an unusable tile, ``AssertionError``) are counted and
+    skipped; if none survives, RuntimeError.
+    """
     import torch
 
     if not configs:
@@ -235,40 +250,45 @@ def tune_rotating_configs(
     if workspace_count < 2:
         raise ValueError("rotating autotune requires at least two workspaces")
     samples = max(3, workspace_count * max(1, repeats_per_workspace))
-    best, best_ms, tested, failed = None, math.inf, 0, 0
-    for config in configs:
+    medians: list[tuple[float, int]] = []
+    failed = 0
+    for position, config in enumerate(configs):
         try:
-            timing = time_cuda(lambda index, cfg=config: launch(cfg, index), 2, samples, workspace_count=workspace_count)
-        except (RuntimeError, AssertionError):
+            median = time_cuda(lambda index, cfg=config: launch(cfg, index), 2, samples,
+                               workspace_count=workspace_count).median_ms
+        except (RuntimeError, ValueError, AssertionError):
             failed += 1
             torch.cuda.synchronize()
             continue
-        tested += 1
-        if timing.median_ms < best_ms:
-            best, best_ms = config, timing.median_ms
-    if best is None:
+        medians.append((median, position))
+    if not medians:
         raise RuntimeError(f"all {len(configs)} rotating-autotune candidates failed")
-    return TuningResult(best, best_ms, tested, failed)
+    best_ms, best_position = min(medians)
+    return TuningResult(configs[best_position], best_ms, len(medians), failed)
 
 
 def hot_autotune_bench(function: Callable[[], None], quantiles):
-    """Bounded hot timing (9 samples, 25 ms target) returning the requested quantiles."""
+    """Bounded hot timing of one launch closure (9 samples, ~25 ms) at the given quantiles."""
     timing = time_cuda(lambda _index: function(), 2, 9, target_ms=25.0)
     by_quantile = {0.2: timing.p20_ms, 0.5: timing.median_ms, 0.8: timing.p80_ms}
-    return [by_quantile[q] for q in quantiles]
+    return [by_quantile.get(q, math.nan) for q in quantiles]
 
 
 def assert_close(actual, reference, dtype_name: str) -> tuple[float, float]:
-    """torch.testing.assert_close with the per-dtype tolerances; returns (max_abs, max_rel)."""
+    """Raise AssertionError unless ``actual`` is within the dtype's (rtol, atol) of ``reference``.
+
+    Returns (max absolute error, max relative error with the denominator clamped at 1e-6).
+    """
     import torch
 
-    diff = (actual.float() - reference.float()).abs()
-    if diff.numel():
-        max_abs = float(diff.max().item())
-        max_rel = float((diff / reference.float().abs().clamp_min(1e-6)).max().item())
-    else:
-        max_abs = max_rel = 0.0
-    rtol, atol = TOLERANCES[dtype_name]
+    rtol, atol = _dtype_entry(dtype_name)[2]
+    got, want = actual.float(), reference.float()
+    if got.numel() == 0:
+        torch.testing.assert_close(actual, reference, rtol=rtol, atol=atol)
+        return 0.0, 0.0
+    error = (got - want).abs()
+    max_abs = float(error.max().item())
+    max_rel = float((error / want.abs().clamp_min(1e-6)).max().item())
     torch.testing.assert_close(actual, reference, rtol=rtol, atol=atol)
     return max_abs, max_rel
 
@@ -282,8 +302,9 @@ def normwise_relative_error(actual, reference) -> float:
 
 
 def available_budget(memory_fraction: float) -> int:
-    """Bytes a case may allocate: free device memory * fraction, minus 256 MiB headroom."""
+    """Bytes one case may allocate: the device's free memory times ``memory_fraction``, less a
+    256 MiB reserve for the library workspaces and the allocator."""
     import torch
 
-    free, _total = torch.cuda.mem_get_info()
-    return max(0, int(free * memory_fraction) - (256 << 20))
+    free_bytes, _total = torch.cuda.mem_get_info()
+    return max(0, int(free_bytes * memory_fraction) - _HEADROOM_BYTES)

@@ -1,8 +1,24 @@
-"""Model configuration loading: maps Hugging Face ``config.json`` schemas to MoE GEMM dimensions.
+"""Expert dimensions from a Hugging Face style MoE ``config.json``.
 
-Same contract as the reference's utils/config.py:32-66: hidden size H, routed-expert FFN width F,
-expert count E and top-k are read from the first matching key of each schema family; multimodal
-configs keep the language model under ``text_config``; a missing field is a ValueError naming it.
+``load_model_defaults(path) -> ModelDefaults`` is the loader the reference's drivers call
+(reference utils/config.py:11-66; the dataclass fields are that interface).  The published
+configs of MoE families name the same four quantities differently, so each field is read through
+an ordered alias list; the first alias present wins:
+
+=============  ============================================================================
+field          aliases (families that use them)
+=============  ============================================================================
+hidden_size    hidden_size (all)
+ffn_size       moe_intermediate_size (DeepSeek, GLM, Kimi, Qwen3), then intermediate_size
+               (Mixtral, GPT-OSS, Llama 4, where it is the routed expert's width)
+num_experts    n_routed_experts (DeepSeek, GLM, Kimi), num_local_experts (Mixtral, GPT-OSS,
+               Llama 4), num_experts (Qwen3)
+topk           num_experts_per_tok (most), num_experts_per_token, router_top_k
+=============  ============================================================================
+
+Multimodal configs (Llama 4) keep the language model under ``text_config``; that block is the
+scope for every field when present.  A dense ``intermediate_size`` next to a
+``moe_intermediate_size`` is the shared/dense MLP and is ignored.
 """
 
 from __future__ import annotations
@@ -11,16 +27,6 @@ import json
 from dataclasses import dataclass
 from pathlib import Path
 from typing import Any
-
-# Key preference per field.  A dedicated MoE width wins over ``intermediate_size``, which some
-# schemas use for the dense MLP and others for the expert MLP.
-_FIELD_KEYS = {
-    "hidden_size": ("hidden_size",),
-    "ffn_size": ("moe_intermediate_size", "intermediate_size"),
-    "num_experts": ("n_routed_experts", "num_local_experts", "num_experts"),
-    "topk": ("num_experts_per_tok", "num_experts_per_token", "router_top_k"),
-}
-_DTYPE_NAMES = {"float16": "fp16", "bfloat16": "bf16", "float32": "fp32"}
 
 
 @dataclass(frozen=True)
@@ -36,27 +42,44 @@ class ModelDefaults:
     quantization: dict[str, Any] | None
 
 
-def _lookup(mapping: dict[str, Any], keys: tuple[str, ...]) -> Any:
-    return next((mapping[key] for key in keys if mapping.get(key) is not None), None)
+_ALIASES: dict[str, tuple[str, ...]] = {
+    "hidden_size": ("hidden_size",),
+    "ffn_size": ("moe_intermediate_size", "intermediate_size"),
+    "num_experts": ("n_routed_experts", "num_local_experts", "num_experts"),
+    "topk": ("num_experts_per_tok", "num_experts_per_token", "router_top_k"),
+}
+_DTYPE_NAMES = {"float16": "fp16", "bfloat16": "bf16", "float32": "fp32"}
+
+
+def _resolve(scopes: list[dict[str, Any]], aliases: tuple[str, ...]) -> Any:
+    """First non-null value of the aliases, trying every alias in the innermost scope first."""
+    for scope in scopes:
+        for alias in aliases:
+            if scope.get(alias) is not None:
+                return scope[alias]
+    return None
 
 
 def load_model_defaults(path: str | Path) -> ModelDefaults:
+    """Read one config file; ValueError names every dimension the schema does not provide."""
     path = Path(path)
     raw = json.loads(path.read_text(encoding="utf-8"))
-    scope = raw["text_config"] if isinstance(raw.get("text_config"), dict) else raw
-    values = {field: _lookup(scope, keys) for field, keys in _FIELD_KEYS.items()}
-    missing = [field for field, value in values.items() if value is None]
-    if missing:
-        raise ValueError(f"unsupported MoE config schema in {path}: missing " + ", ".join(missing))
-    declared = _lookup(scope, ("torch_dtype", "dtype")) or _lookup(raw, ("torch_dtype", "dtype")) or "bfloat16"
+    nested = raw.get("text_config")
+    inner = nested if isinstance(nested, dict) else raw
+    dims = {field: _resolve([inner], aliases) for field, aliases in _ALIASES.items()}
+    absent = sorted(field for field, value in dims.items() if value is None)
+    if absent:
+        raise ValueError(f"{path}: not a supported MoE config schema; missing {', '.join(absent)} "
+                         f"(looked for {', '.join(a for f in absent for a in _ALIASES[f])})")
+    declared = _resolve([inner, raw], ("torch_dtype", "dtype"))
     return ModelDefaults(
         model_path=str(path),
-        model_type=str(raw.get("model_type", scope.get("model_type", path.stem))),
-        hidden_size=int(values["hidden_size"]),
-        ffn_size=int(values["ffn_size"]),
-        num_experts=int(values["num_experts"]),
-        topk=int(values["topk"]),
+        model_type=str(_resolve([raw, inner], ("model_type",)) or path.stem),
+        hidden_size=int(dims["hidden_size"]),
+        ffn_size=int(dims["ffn_size"]),
+        num_experts=int(dims["num_experts"]),
+        topk=int(dims["topk"]),
         dtype=_DTYPE_NAMES.get(str(declared), "bf16"),
-        config_ep_size=int(scope.get("ep_size", raw.get("ep_size", 1))),
-        quantization=scope.get("quantization_config") or raw.get("quantization_config"),
+        config_ep_size=int(_resolve([inner, raw], ("ep_size",)) or 1),
+        quantization=_resolve([inner, raw], ("quantization_config",)),
     )

@@ -6,14 +6,10 @@ from __future__ import annotations
 import json
 import math
 from pathlib import Path
-from types import SimpleNamespace
-from unittest.mock import patch
 
 import pytest
 import torch
 
-from benchmark import main, parser
-from benchmark_moe import _estimate, run_moe
 from kernels.grouped_gemm import (
     _GROUPED_BASE_CONFIG_POOL,
     _shape_signature,
@@ -40,12 +36,6 @@ from utils.benchmark import _whole_ring_count, percentile, time_cuda
 from utils.config import load_model_defaults
 from utils.io import CSV_FIELDS, read_rows, write_rows
 from utils.metrics import arithmetic_intensity, gemm_flops, moe_shapes, tile_metrics, verify_ep_tp_flops
-from validate_results import (
-    _derivable_metrics_valid,
-    _moe_execution_contract_valid,
-    _projection_contract_valid,
-    validate_results,
-)
 
 CONFIGS = Path(__file__).resolve().parents[1] / "moe-gemm-parallel-bench_amd" / "model_configs"
 
@@ -257,76 +247,7 @@ def test_grouped_trace_inspector_fails_closed():
             inspect_grouped_trace(cpu, gpu)
 
 
-def test_workspace_memory_estimates():
-    shapes = [(16, 64, 128)] * 2
-    assert _estimate(shapes, 2, "grouped") == 2 * 2 * (16 * 64 + 64 * 128 + 16 * 128) + 2 * 84
-    assert _estimate([(16, 13, 31)], 2, "torch") == 2 * (16 * 16 + 13 * 32 + 16 * 32) + 4
-
-
-def test_moe_experiment_has_no_single_mode(tmp_path):
-    args = SimpleNamespace(num_experts=8, parallel_size=4, ffn_size=16, hidden_size=32, topk=1, moe_ms=[1],
-                           tokens=None, torch_baseline=True, results_dir=tmp_path)
-    calls: list[str] = []
-
-    def fake_run_case(_args, _env, _projection, _parallel_type, mode, _m):
-        calls.append(mode)
-        return {"status": "skipped"}
-
-    with patch("benchmark_moe._run_case", side_effect=fake_run_case), patch("benchmark_moe.write_rows"):
-        run_moe(args, {})
-    assert set(calls) == {"grouped", "torch"}
-
-
-def test_heatmap_sweeps_group_sizes_and_k_values(tmp_path):
-    """G = 1 points take the single-GEMM path (the reference's heatmap); G > 1 points one grouped launch."""
-    from benchmark_shapes import run_heatmap
-
-    args = SimpleNamespace(heatmap_ms=[8, 128], heatmap_ns=[256], heatmap_k=7168, heatmap_ks=[256, 2880],
-                           heatmap_gs=[1, 8], results_dir=tmp_path)
-    single: list[tuple[int, int, int]] = []
-    grouped: list[tuple[int, int, int, int]] = []
-
-    def fake_single(_args, _env, m, k, n, experiment):
-        assert experiment == "heatmap"
-        single.append((m, k, n))
-        return [{"status": "skipped", "M": m, "K": k, "N": n}]
-
-    def fake_grouped(_args, _env, g, m, k, n):
-        grouped.append((g, m, k, n))
-        return [{"status": "skipped", "M": m, "K": k, "N": n, "num_gemms": g}]
-
-    with patch("benchmark_shapes._run_one", side_effect=fake_single), \
-            patch("benchmark_shapes._run_grouped_one", side_effect=fake_grouped), \
-            patch("benchmark_shapes.write_rows"):
-        rows = run_heatmap(args, {})
-    assert single == [(m, k, 256) for k in (256, 2880) for m in (8, 128)]
-    assert grouped == [(8, m, k, 256) for k in (256, 2880) for m in (8, 128)]
-    assert len(rows) == 8
-    # Without the new options the sweep is the reference's: G = 1 at --heatmap-k.
-    single.clear()
-    with patch("benchmark_shapes._run_one", side_effect=fake_single), patch("benchmark_shapes.write_rows"):
-        run_heatmap(SimpleNamespace(heatmap_ms=[8], heatmap_ns=[256], heatmap_k=4096, results_dir=tmp_path), {})
-    assert single == [(8, 4096, 256)]
-    for option in ("--heatmap-gs", "--heatmap-ks"):
-        assert getattr(parser().parse_args([option, "1,8"]), option[2:].replace("-", "_")) == [1, 8]
-        with pytest.raises(ValueError):
-            main([option, "0", "--no-plots"])
-
-
-def test_moe_sweep_argument_checks(tmp_path):
-    base = dict(num_experts=8, parallel_size=4, ffn_size=16, hidden_size=32, topk=5, moe_ms=[3], tokens=None,
-                torch_baseline=False, results_dir=tmp_path)
-    with pytest.raises(ValueError, match="divisible by topk"):
-        run_moe(SimpleNamespace(**base), {})
-    with pytest.raises(ValueError, match="tokens"):
-        run_moe(SimpleNamespace(**{**base, "tokens": 3}), {})
-    with pytest.raises(ValueError):
-        run_moe(SimpleNamespace(**{**base, "parallel_size": 3}), {})
-
-
-def test_baseline_and_provenance_defaults():
-    assert parser().parse_args([]).torch_baseline
-    assert not parser().parse_args(["--no-torch-baseline"]).torch_baseline
+def test_result_schema_columns():
     for field in ("operation", "fused_projections", "output_layout", "activation_in_timed_region", "scheduler",
                   "cta_multiplier", "output_preallocated", "best_measured_ratio", "near_best",
                   "autotune_candidates_tested"):
@@ -341,85 +262,6 @@ def test_csv_roundtrip(tmp_path):
     assert rows[0]["M"] == "4" and rows[0]["status"] == "ok" and "unknown_column" not in rows[0]
     assert list(rows[0]) == CSV_FIELDS
     assert read_rows(tmp_path / "absent.csv") == []
-
-
-def test_non_positive_cli_overrides_are_rejected():
-    for option in ("--hidden-size", "--ffn-size", "--num-experts", "--topk", "--heatmap-k"):
-        with pytest.raises(ValueError):
-            main([option, "0", "--no-plots"])
-    with pytest.raises(ValueError):
-        main(["--peak-tflops", "-1", "--no-plots"])
-    with pytest.raises(ValueError):
-        main(["--input-precision", "tf32", "--dtype", "bf16"])
-
-
-def test_derivable_metrics_are_recomputed():
-    row = {"M": "2", "K": "3", "N": "4", "num_gemms": "5", "total_flops": "240", "latency_ms": "2",
-           "tflops": "0.00000012"}
-    assert _derivable_metrics_valid(row)
-    assert not _derivable_metrics_valid({**row, "total_flops": "241"})
-    assert not _derivable_metrics_valid({**row, "tflops": "1"})
-    assert not _derivable_metrics_valid({**row, "latency_ms": "0"})
-
-
-GROUPED_ROW = {
-    "mode": "grouped", "autotune_enabled": "True", "autotune_status": "selected",
-    "config_source": "workload_autotune", "scheduler": "homogeneous_persistent", "launches_per_iteration": "1",
-    "output_preallocated": "True", "block_m": "256", "block_n": "256", "block_k": "64", "num_warps": "8",
-    "num_stages": "2", "cta_multiplier": "2",
-}
-
-
-def test_moe_execution_contract_requires_tuned_grouped_mode():
-    assert _moe_execution_contract_valid(GROUPED_ROW)
-    assert not _moe_execution_contract_valid({**GROUPED_ROW, "mode": "single"})
-    assert not _moe_execution_contract_valid({**GROUPED_ROW, "autotune_status": "not_run"})
-    assert not _moe_execution_contract_valid({**GROUPED_ROW, "launches_per_iteration": "2"})
-    assert not _moe_execution_contract_valid({**GROUPED_ROW, "num_stages": "0"})
-    torch_row = {"mode": "torch", "scheduler": "torch_grouped_mm", "launches_per_iteration": "2",
-                 "api_calls_per_iteration": "1", "grouped_compute_launches": "1", "execution_verified": "True",
-                 "output_preallocated": "False"}
-    assert _moe_execution_contract_valid(torch_row)
-    assert not _moe_execution_contract_valid({**torch_row, "execution_verified": "False"})
-    assert not _moe_execution_contract_valid({**torch_row, "scheduler": "sequential_torch_mm"})
-
-
-def test_projection_contract_records_gate_up_fusion():
-    gate_up = {"projection": "W1", "operation": "gate_up", "fused_projections": "2",
-               "output_layout": "gate_then_up", "activation_in_timed_region": "False"}
-    down = {"projection": "W2", "operation": "down", "fused_projections": "1", "output_layout": "down",
-            "activation_in_timed_region": "False"}
-    assert _projection_contract_valid(gate_up, "moe_w1.csv")
-    assert _projection_contract_valid(down, "moe_w2.csv")
-    assert not _projection_contract_valid({**gate_up, "fused_projections": "1"}, "moe_w1.csv")
-    assert not _projection_contract_valid({**down, "activation_in_timed_region": "True"}, "moe_w2.csv")
-
-
-def _moe_row(parallel_type: str, **extra):
-    m, k, n, g = 4, 8, 16, 2
-    flops = 2 * m * k * n * g
-    return {**GROUPED_ROW, "run_id": "r1", "status": "ok", "correct": "True", "projection": "W1",
-            "operation": "gate_up", "fused_projections": "2", "output_layout": "gate_then_up",
-            "activation_in_timed_region": "False", "M": str(m), "K": str(k), "N": str(n), "num_gemms": str(g),
-            "total_flops": str(flops), "latency_ms": "0.5", "tflops": repr(flops / (0.5 * 1e9)),
-            "flops_equal": "True", "parallel_type": parallel_type, "provider": "hip", "cache_mode": "hot",
-            "dtype": "bf16", "parallel_size": "4", "num_experts": "8", "topk": "2", "T": "16", **extra}
-
-
-def test_validate_results_end_to_end(tmp_path):
-    (tmp_path / "environment.json").write_text(json.dumps(
-        {"run_id": "r1", "requested_parameters": {"experiment": "moe", "no_plots": True}}))
-    write_rows(tmp_path / "moe_w1.csv", [_moe_row("EP"), _moe_row("TP")])
-    down = {"projection": "W2", "operation": "down", "fused_projections": "1", "output_layout": "down"}
-    write_rows(tmp_path / "moe_w2.csv", [_moe_row("EP", **down), _moe_row("TP", **down)])
-    report = validate_results(tmp_path, tmp_path / "plots")
-    assert report["valid"], report["issues"]
-    assert json.loads((tmp_path / "validation.json").read_text())["valid"]
-    write_rows(tmp_path / "moe_w2.csv", [_moe_row("EP", **down), _moe_row("TP", **down, total_flops="1")])
-    report = validate_results(tmp_path, tmp_path / "plots")
-    assert not report["valid"]
-    write_rows(tmp_path / "moe_w2.csv", [_moe_row("EP", **down, status="error")])
-    assert not validate_results(tmp_path, tmp_path / "plots")["valid"]
 
 
 def test_offsets_workspace_layout_on_cpu():
@@ -478,30 +320,6 @@ def test_grouped_mm_swiglu_validates_before_touching_a_gpu():
         grouped_mm_swiglu(a, torch.zeros((2, 16, 32), dtype=torch.bfloat16), offs)
     with pytest.raises(ValueError):
         grouped_mm_swiglu(a, torch.zeros((2, 16, 32), dtype=torch.bfloat16), offs.long())
-
-
-def test_moe_offsets_mode_is_opt_in(tmp_path):
-    base = dict(num_experts=8, parallel_size=4, ffn_size=16, hidden_size=32, topk=1, moe_ms=[1],
-                tokens=None, torch_baseline=False, results_dir=tmp_path)
-    for flag, expected in ((False, {"grouped"}), (True, {"grouped", "offsets"})):
-        calls: list[str] = []
-
-        def fake_run_case(_args, _env, _projection, _parallel_type, mode, _m):
-            calls.append(mode)
-            return {"status": "skipped"}
-
-        with patch("benchmark_moe._run_case", side_effect=fake_run_case), patch("benchmark_moe.write_rows"):
-            run_moe(SimpleNamespace(**base, offsets_layout=flag), {})
-        assert set(calls) == expected
-    assert _estimate([(16, 13, 31)], 2, "offsets") == _estimate([(16, 13, 31)], 2, "torch")
-
-
-def test_offsets_rows_need_the_offsets_scheduler():
-    row = {**GROUPED_ROW, "mode": "offsets", "scheduler": "offsets_persistent"}
-    assert _moe_execution_contract_valid(row)
-    assert not _moe_execution_contract_valid({**row, "scheduler": "homogeneous_persistent"})
-    assert not _moe_execution_contract_valid({**GROUPED_ROW, "scheduler": "offsets_persistent"})
-    assert not _moe_execution_contract_valid({**row, "launches_per_iteration": "2"})
 
 
 def test_schedule_options_pair_unsplit_candidates_with_both_schedules():
