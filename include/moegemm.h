@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define MOEGEMM_ABI_VERSION 5
+#define MOEGEMM_ABI_VERSION 6
 
 #define MOEGEMM_OK 0
 #define MOEGEMM_ERR_INVALID (-1)   /* bad shape, pointer, dtype or parameter (Python: ValueError) */
@@ -142,6 +142,27 @@ int moegemm_matmul_splitk(const void* a, const void* b, void* c, int32_t m, int3
                           int32_t block_m, int32_t block_n, int32_t block_k, int32_t group_size_m,
                           int32_t num_warps, int32_t num_stages, int32_t splits, int32_t grid_size,
                           void* workspace, int64_t workspace_bytes, void* stream);
+/*
+ * moegemm_matmul_splitk without the workspace argument: the partials and tile counters live in a
+ * static device array of MOEGEMM_NOALLOC_SCRATCH_BYTES inside the library (one per GPU, held until
+ * the process ends), so the call allocates nothing, not even on its first use.  No counterpart in
+ * the reference: it is for callers that cannot allocate (code under HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc).  Limits and rules:
+ *   - a launch whose split partials need more than MOEGEMM_NOALLOC_SCRATCH_BYTES (256 KiB of
+ *     counters + tiles * splits * block_m * block_n * 4 bytes) is rejected with
+ *     MOEGEMM_ERR_INVALID before anything runs;
+ *   - every call on one GPU shares that GPU's area: calls that overlap on one GPU (different
+ *     streams or threads without ordering) race and may produce wrong results;
+ *   - the first call on a GPU also launches one small kernel on `stream` that clears the counters
+ *     (later launches leave them zero); the results equal moegemm_matmul_splitk's bit for bit.
+ */
+#define MOEGEMM_NOALLOC_SCRATCH_BYTES (64 * 1024 * 1024 + 256 * 1024)
+int moegemm_matmul_splitk_noalloc(const void* a, const void* b, void* c, int32_t m, int32_t n, int32_t k,
+                                  int64_t stride_am, int64_t stride_ak, int64_t stride_bk,
+                                  int64_t stride_bn, int64_t stride_cm, int64_t stride_cn, int32_t dtype,
+                                  int32_t block_m, int32_t block_n, int32_t block_k, int32_t group_size_m,
+                                  int32_t num_warps, int32_t num_stages, int32_t splits, int32_t grid_size,
+                                  void* stream);
 /* Homogeneous grouped counterpart (equal contiguous problems, vector_layout must be 1). */
 int moegemm_grouped_gemm_splitk(const int64_t* a_ptrs, const int64_t* b_ptrs, const int64_t* c_ptrs,
                                 int32_t problem_count, int32_t m, int32_t n, int32_t k,

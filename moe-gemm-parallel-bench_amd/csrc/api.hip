@@ -9,6 +9,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/moegemm.h"
@@ -112,6 +113,50 @@ int setup_splits(KParams& p, int64_t tiles, int32_t k, int32_t splits, int32_t b
   p.splits = (int32_t)effective;
   p.k_chunk = (int32_t)chunk;
   p.total_tiles = (int32_t)tiles;
+  return MOEGEMM_OK;
+}
+
+// Static split-K scratch of the no-allocation entry point: the same layout as a caller workspace
+// (counters, then partials).  Each GPU holds its own copy from module load until the process ends.
+// Host code never uses the array's name as an address (in host code it is a stand-in, not device
+// memory): each device's address comes from hipGetSymbolAddress, taken once per device with that
+// device current, and only that address is passed to kernels.
+static __device__ __align__(256) char scratch[MOEGEMM_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_address[kMaxDevices] = {};
+
+__global__ void clear_counters(int32_t* counters, int32_t words) {
+  for (int32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < words; i += gridDim.x * blockDim.x) counters[i] = 0;
+}
+
+// Address of the current device's scratch area.  The first call on a device looks it up and
+// clears the counter area with a kernel on `stream` (so a first call inside graph capture records
+// a kernel, not a memset); every later launch leaves the counters zero again.
+int device_scratch(void* stream, void** out) {
+  int device = -1;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return fail(MOEGEMM_ERR_LAUNCH, "hipGetDevice failed: %s", hipGetErrorString(err));
+  if (device < 0 || device >= kMaxDevices)
+    return fail(MOEGEMM_ERR_INVALID, "device index %d is beyond the %d devices the library tracks", device,
+                kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_address[device]) {
+    void* address = nullptr;
+    err = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !address)
+      return fail(MOEGEMM_ERR_LAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", device,
+                  hipGetErrorString(err));
+    const int32_t words = (int32_t)(kSplitCounterBytes / 4);
+    hipLaunchKernelGGL(clear_counters, dim3(64), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                       static_cast<int32_t*>(address), words);
+    err = hipGetLastError();
+    if (err != hipSuccess)
+      return fail(MOEGEMM_ERR_LAUNCH, "clearing the scratch counters failed: %s", hipGetErrorString(err));
+    g_scratch_address[device] = address;
+  }
+  *out = g_scratch_address[device];
   return MOEGEMM_OK;
 }
 
@@ -272,7 +317,7 @@ int moegemm_splitk_workspace_bytes(int32_t tiles, int32_t splits, int32_t block_
   return MOEGEMM_OK;
 }
 
-int moegemm_matmul_splitk(const void* a, const void* b, void* c, int32_t m, int32_t n, int32_t k, int64_t stride_am,
+static int matmul_splitk_impl(const void* a, const void* b, void* c, int32_t m, int32_t n, int32_t k, int64_t stride_am,
                           int64_t stride_ak, int64_t stride_bk, int64_t stride_bn, int64_t stride_cm,
                           int64_t stride_cn, int32_t dtype, int32_t block_m, int32_t block_n, int32_t block_k,
                           int32_t group_size_m, int32_t num_warps, int32_t num_stages, int32_t splits,
@@ -309,6 +354,41 @@ int moegemm_matmul_splitk(const void* a, const void* b, void* c, int32_t m, int3
   const int64_t units = (int64_t)p.total_tiles * p.splits;
   const int grid = grid_size <= 0 || grid_size > units ? (int)units : grid_size;
   return launch(e, p, grid, true, stream);
+}
+
+int moegemm_matmul_splitk(const void* a, const void* b, void* c, int32_t m, int32_t n, int32_t k, int64_t stride_am,
+                          int64_t stride_ak, int64_t stride_bk, int64_t stride_bn, int64_t stride_cm,
+                          int64_t stride_cn, int32_t dtype, int32_t block_m, int32_t block_n, int32_t block_k,
+                          int32_t group_size_m, int32_t num_warps, int32_t num_stages, int32_t splits,
+                          int32_t grid_size, void* workspace, int64_t workspace_bytes, void* stream) {
+  return matmul_splitk_impl(a, b, c, m, n, k, stride_am, stride_ak, stride_bk, stride_bn, stride_cm, stride_cn, dtype,
+                            block_m, block_n, block_k, group_size_m, num_warps, num_stages, splits, grid_size,
+                            workspace, workspace_bytes, stream);
+}
+
+int moegemm_matmul_splitk_noalloc(const void* a, const void* b, void* c, int32_t m, int32_t n, int32_t k,
+                                  int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
+                                  int64_t stride_cm, int64_t stride_cn, int32_t dtype, int32_t block_m,
+                                  int32_t block_n, int32_t block_k, int32_t group_size_m, int32_t num_warps,
+                                  int32_t num_stages, int32_t splits, int32_t grid_size, void* stream) {
+  void* area = nullptr;
+  int rc = device_scratch(stream, &area);
+  if (rc != MOEGEMM_OK) return rc;
+  // The split count that will run (trailing empty K ranges dropped) decides the bytes needed; reject
+  // a launch whose partials would not fit the static area before touching it.
+  if (splits >= 1 && splits <= 64 && block_m > 0 && block_n > 0 && block_k > 0 && m > 0 && n > 0 && k > 0) {
+    const int64_t chunk = cdiv(cdiv(k, splits), block_k) * block_k;
+    const int64_t effective = cdiv(k, chunk);
+    const int64_t need = splitk_bytes(cdiv(m, block_m) * cdiv(n, block_n), effective, block_m, block_n);
+    if (effective > 1 && need > MOEGEMM_NOALLOC_SCRATCH_BYTES)
+      return fail(MOEGEMM_ERR_INVALID,
+                  "split-K launch needs %lld bytes of scratch, beyond the %lld-byte static area of the "
+                  "no-allocation entry point; use moegemm_matmul_splitk with a workspace",
+                  (long long)need, (long long)MOEGEMM_NOALLOC_SCRATCH_BYTES);
+  }
+  return matmul_splitk_impl(a, b, c, m, n, k, stride_am, stride_ak, stride_bk, stride_bn, stride_cm, stride_cn, dtype,
+                            block_m, block_n, block_k, group_size_m, num_warps, num_stages, splits, grid_size, area,
+                            MOEGEMM_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 int moegemm_grouped_gemm_splitk(const int64_t* a_ptrs, const int64_t* b_ptrs, const int64_t* c_ptrs,

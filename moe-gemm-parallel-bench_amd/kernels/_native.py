@@ -15,7 +15,7 @@ from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().with_name("libmoegemm.so")
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 OK = 0
 ERR_INVALID = -1
 ERR_NO_KERNEL = -2
@@ -60,6 +60,11 @@ SIGNATURES = {
         ctypes.c_int,
         [_vp, _vp, _vp, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i32,
          _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _vp],
+    ),
+    "moegemm_matmul_splitk_noalloc": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i32,
+         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
     ),
     "moegemm_grouped_gemm_splitk": (
         ctypes.c_int,
@@ -200,6 +205,7 @@ def splitk_workspace(device, stream_handle: int, nbytes: int):
 # Work-stealing tile queues, one per (device, stream), zeroed once and never released (launches
 # leave them zero; a captured graph keeps a valid address).
 QUEUE_BYTES = 256
+NOALLOC_SCRATCH_BYTES = 64 * 1024 * 1024 + 256 * 1024  # MOEGEMM_NOALLOC_SCRATCH_BYTES
 TILE_SCHEDULES = ("static", "stealing")
 _TILE_QUEUES: dict[tuple[int, int], object] = {}
 
