@@ -27,11 +27,13 @@
 //    silu(gate) * up from the fp32 accumulators in registers and stores F-wide rows.  Needs an
 //    even FN and F a multiple of 8 (checked by the host).
 //  * Split-K units (KParams::splits > 1) end with split_store instead of the C store: the fp32
-//    partial tile goes to the caller's workspace, a device-scope release fence orders it before
-//    one atomic increment of the tile's counter, and the unit that brings the counter to `splits`
-//    re-arms it (writes 0), fences (device-scope acquire; the other units skip it, so a tile
-//    costs one cache invalidation) and sums all partials of the tile in split order —
-//    the same order whichever unit is last, so results are deterministic — then casts and stores C.
+//    partial tile goes to the caller's workspace with device-coherent (sc1) 16-byte stores, the
+//    workgroup waits for them to complete before one atomic increment of the tile's counter, and
+//    the unit that brings the counter to `splits` re-arms it (writes 0) and reads all partials of
+//    the tile with device-coherent loads, summing them in split order — the same order whichever
+//    unit is last, so results are deterministic — then casts and stores C.  No L2 writeback or
+//    invalidation is involved (a device-scope fence would write back or invalidate the whole L2
+//    of the XCD in every unit).
 //  * C epilogue through LDS (STAGED_OK tiles): the 32x32 / 16x16 accumulator layout leaves each
 //    lane 4 consecutive columns of one row, so direct stores write 8 bytes per row per lane and one
 //    store instruction touches 32 (or 16) rows.  Instead each wave converts its WTM x WTN sub-tile
@@ -52,6 +54,8 @@ namespace moegemm {
 // Raw buffer resource word 3 for gfx9 untyped buffer loads (32-bit data format).
 constexpr uint32_t kBufferFlags = 0x00020000u;
 constexpr uint32_t kOutOfRange = 0x80000000u;
+// Cache-policy operand of the buffer load/store builtins: sc1, device (agent) scope coherence.
+constexpr int kDeviceCoherent = 16;
 
 __device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
 
@@ -74,6 +78,18 @@ __device__ __forceinline__ void dma_copy16(u32x4_t rsrc, uint32_t voffset, uint3
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voffset), "s"(rsrc), "s"(lds)
+               : "memory", "m0");
+#pragma clang diagnostic pop
+}
+
+// dma_copy16 with device-coherent (sc1) reads: for data that other workgroups, possibly on other
+// XCDs, wrote with sc1 stores (the split-K partials).
+__device__ __forceinline__ void dma_copy16_coherent(u32x4_t rsrc, uint32_t voffset, uint32_t lds) {
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen sc1 lds"
                :
                : "v"(voffset), "s"(rsrc), "s"(lds)
                : "memory", "m0");
@@ -308,29 +324,58 @@ struct FastTile {
   // IEEE divide: the result is rounded to 16 bits, far coarser than either error.
   __device__ static __forceinline__ float silu(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
+  // Split-K reduction through LDS: after the K loop the DMA ring is free, and each wave takes
+  // RED_SLOTS 1 KiB slots of it.  The wave's share of one partial is RED_CH 1 KiB chunks (each lane
+  // fetches the 16 bytes of its own accumulator chunk, landing at slot + 16 * lane).  A round copies
+  // RED_R splits x RED_CB chunks (at most RED_CAP copies in flight per wave), waits once, and adds
+  // them from LDS, so many partials share one memory round trip.  The sum of every element runs in
+  // split order.  KEEP_OWN tiles add their own partial from the accumulators; larger tiles read it
+  // back like the others, so that the accumulators are dead and the registers free.
+  static constexpr int RED_CH = FM * FN * (ACC / 4);
+  static constexpr int RED_SLOTS = (STAGES * STAGE_BYTES / NW) / 1024;
+  static constexpr int RED_CAP = RED_SLOTS < 48 ? RED_SLOTS : 48;
+  static constexpr int RED_CB = RED_CH < RED_CAP ? RED_CH : RED_CAP;
+  static constexpr int RED_R = RED_CAP / RED_CB;
+  static constexpr bool KEEP_OWN = 2 * FM * FN * ACC <= 160;
+  static_assert(RED_CAP >= 1 && RED_R >= 1, "at least one 1 KiB slot per wave for the split-K reduction");
+
+  // Byte offset, inside one partial tile, of this lane's 16-byte accumulator chunk (fm, fn, q).
+  // Partials are private scratch, laid out in accumulator order [wave][chunk][lane][4 floats]: each
+  // wave's store or load of one chunk is one contiguous 1 KiB access (a row-major tile would give
+  // every instruction 16 bytes in each of 32 rows).  Every unit of a tile runs the same tile, so
+  // chunk (wave, c) holds the same output elements in every split's partial.
+  __device__ static __forceinline__ int chunk_offset(int fm, int fn, int q, int wave) {
+    const int lane = threadIdx.x & 63;
+    const int c = (fm * FN + fn) * (ACC / 4) + q;
+    return ((wave * RED_CH + c) * 64 + lane) * 16;
+  }
+
   __device__ static __forceinline__ void split_store(const acc_t (&acc)[FM][FN], const ProblemDesc& pd, int m0,
-                                                     int n0, int wave_m, int wave_n) {
+                                                     int n0, int wave_m, int wave_n, char* smem) {
     __shared__ int s_last;
     const int lane = threadIdx.x & 63;
-    // Partial slot of split sp: [tiles][splits][BM * BN].
-    auto slot = [&](int sp) -> float* { return pd.partials + ((int64_t)pd.tile * pd.splits + sp) * (BM * BN); };
-    float* mine = slot(pd.split);
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    // Partial slot of split sp: [tiles][splits][BM * BN] floats.
+    constexpr uint32_t kSlotBytes = BM * BN * 4;
+    auto slot_base = [&](int sp) { return pd.partials + ((int64_t)pd.tile * pd.splits + sp) * (BM * BN); };
+    const auto mine = __builtin_amdgcn_make_buffer_rsrc(slot_base(pd.split), (short)0, (int)kSlotBytes,
+                                                        (int)kBufferFlags);
 #pragma unroll
-    for (int fm = 0; fm < FM; ++fm) {
-      const int rl = wave_m * WTM + fm * MI + (lane % MI);
+    for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
       for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
         for (int q = 0; q < ACC / 4; ++q) {
-          const int cl = wave_n * WTN + fn * MI + ((MI == 32) ? (q * 8 + (lane >> 5) * 4) : ((lane >> 4) * 4));
           const f32x4_t v = {acc[fm][fn][q * 4 + 0], acc[fm][fn][q * 4 + 1], acc[fm][fn][q * 4 + 2],
                              acc[fm][fn][q * 4 + 3]};
-          *MOEGEMM_GLOBAL(f32x4_t, mine + rl * BN + cl) = v;
+          __builtin_amdgcn_raw_buffer_store_b128(v, mine, chunk_offset(fm, fn, q, wave), 0,
+                                                 kDeviceCoherent);
         }
-    }
-    // Release (device scope): this unit's partial is written back before the counter moves.  Only
-    // the last unit acquires, so only one cache invalidation per tile.
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    // The partials are device-coherent (sc1) stores, the encoding of relaxed agent-scope atomic
+    // stores: once this wave's stores have completed they are visible to sc1 loads from any XCD,
+    // so no L2 writeback (release fence) is needed.  The barrier makes every wave's stores complete
+    // before the counter moves.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (threadIdx.x == 0) {
       const int last = atomicAdd(pd.counters + pd.tile, 1) == pd.splits - 1;
@@ -339,9 +384,10 @@ struct FastTile {
     }
     __syncthreads();
     if (!s_last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    // Sum the partials in split order, one whole partial tile at a time so that all of its loads
-    // are in flight together, into a register copy of the tile.
+    // The last unit reads the other partials with device-coherent (sc1) loads, issued after the
+    // counter showed all other units' stores complete: no L2 invalidation (acquire fence) is
+    // needed.  Every element sums the partials in split order, so the result is the same whichever
+    // unit is last.
     acc_t tot[FM][FN];
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm)
@@ -349,20 +395,44 @@ struct FastTile {
       for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
         for (int i = 0; i < ACC; ++i) tot[fm][fn][i] = 0.0f;
-    for (int sp = 0; sp < pd.splits; ++sp) {
-      const float* src = slot(sp);
+    auto add_chunk = [&](int fm, int fn, int q, const f32x4_t& v) {
 #pragma unroll
-      for (int fm = 0; fm < FM; ++fm) {
-        const int rl = wave_m * WTM + fm * MI + (lane % MI);
+      for (int i = 0; i < 4; ++i) tot[fm][fn][q * 4 + i] += v[i];
+    };
+    char* region = smem + wave * RED_SLOTS * 1024;
+    const uint32_t region_lds = lds_address(region);
 #pragma unroll
-        for (int fn = 0; fn < FN; ++fn)
+    for (int cb = 0; cb < RED_CH; cb += RED_CB) {
+      for (int g0 = 0; g0 < pd.splits; g0 += RED_R) {
+        const int count = min(RED_R, pd.splits - g0);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the previous round's LDS reads are done
+        for (int r = 0; r < count; ++r) {
+          const int sp = g0 + r;
+          if (KEEP_OWN && sp == pd.split) continue;
+          const u32x4_t rs = make_rsrc(slot_base(sp), kSlotBytes);
 #pragma unroll
-          for (int q = 0; q < ACC / 4; ++q) {
-            const int cl = wave_n * WTN + fn * MI + ((MI == 32) ? (q * 8 + (lane >> 5) * 4) : ((lane >> 4) * 4));
-            const f32x4_t v = *MOEGEMM_GLOBAL(const f32x4_t, src + rl * BN + cl);
+          for (int i = 0; i < RED_CB; ++i)
+            if (cb + i < RED_CH)
+              dma_copy16_coherent(rs, (uint32_t)(((wave * RED_CH + cb + i) * 64 + lane) * 16),
+                                  region_lds + (uint32_t)((r * RED_CB + i) * 1024));
+        }
+        wait_vmcnt<0>();
+        compiler_fence();
+        for (int r = 0; r < count; ++r) {
+          const bool own = KEEP_OWN && g0 + r == pd.split;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) tot[fm][fn][q * 4 + i] += v[i];
+          for (int i = 0; i < RED_CB; ++i) {
+            const int c = cb + i;
+            if (c >= RED_CH) continue;
+            const int fm = c / (FN * (ACC / 4)), fn = (c / (ACC / 4)) % FN, q = c % (ACC / 4);
+            if (own)
+              add_chunk(fm, fn, q, f32x4_t{acc[fm][fn][q * 4 + 0], acc[fm][fn][q * 4 + 1], acc[fm][fn][q * 4 + 2],
+                                           acc[fm][fn][q * 4 + 3]});
+            else
+              add_chunk(fm, fn, q, *reinterpret_cast<const f32x4_t*>(region + (r * RED_CB + i) * 1024 + lane * 16));
           }
+        }
+        compiler_fence();
       }
     }
 #pragma unroll
@@ -441,7 +511,7 @@ struct FastTile {
                                                     int n0, int wave_m, int wave_n, char* smem) {
     const int lane = threadIdx.x & 63;
     if (pd.splits > 1) {
-      split_store(acc, pd, m0, n0, wave_m, wave_n);
+      split_store(acc, pd, m0, n0, wave_m, wave_n, smem);
       return;
     }
     if constexpr (SWIGLU_OK) {

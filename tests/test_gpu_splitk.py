@@ -160,3 +160,23 @@ def test_launches_of_different_tile_counts_share_one_workspace():
         launch_matmul(a, b, c, cfg, autotune=False, split_k=splits)
         torch.cuda.synchronize()
         assert torch.equal(c.double().cpu(), exact), f"tile {cfg.tile_key} splits {splits}"
+
+
+@pytest.mark.parametrize("splits", [3, 9, 16])
+def test_every_tile_split_known_answer_with_tails(splits):
+    """Every compiled 16-bit tile, forced splits (not multiples of how many partials the last unit
+    stages at once), M and N tails: the reduction's grouping, its own-partial shortcut and the
+    register fallback of the largest tiles all give the exact result."""
+    from kernels import _native
+    from kernels.matmul import KernelConfig, last_matmul_split, launch_matmul
+
+    for bm, bn, bk, warps, stages, _lds, _wm in _native.compiled_kernels(_native.DTYPE_BF16):
+        m, n, k = 2 * bm - 5, 2 * bn + 8, 1280
+        a, b, exact = _known(m, k, n, torch.bfloat16)
+        cfg = KernelConfig(bm, bn, bk, 8, warps, stages, 1)
+        print(f"splitk every tile {cfg.tile_key} splits={splits}", flush=True)
+        c = torch.full((m, n), float("nan"), device="cuda", dtype=torch.bfloat16)
+        launch_matmul(a, b, c, cfg, autotune=False, split_k=splits)
+        torch.cuda.synchronize()
+        assert last_matmul_split() == splits
+        assert torch.equal(c.double().cpu(), exact), f"tile {cfg.tile_key} splits {splits}"
