@@ -16,9 +16,9 @@
 //    rows (A) or of 4x2 row/chunk groups (B transpose reads) fall on distinct banks.
 //  * Global -> LDS staging goes through registers with double-buffered LDS stages: the next K
 //    slice is in flight while MFMAs consume the current one; one workgroup barrier per K slice.
-//  * Persistent schedule: workgroup w of a grid of size G processes tiles v, v+G, v+2G, ... where
-//    v renumbers w so that the 8 XCDs (dispatched round-robin by workgroup id) each own a
-//    contiguous run of tiles per round; neighbouring tiles share A/B panels in that XCD's L2.
+//  * Persistent schedule: each of the 8 XCDs (workgroups are dispatched to them round-robin by
+//    id) owns a contiguous eighth of the tile index space, which its workgroups walk in lockstep;
+//    the tiles of one expert, and so the A/B panels they share, stay in that XCD's L2.
 //  * Generic groups (heterogeneous shapes/strides) map tile -> problem with an LDS prefix sum of
 //    per-problem tile counts and a binary search, instead of a per-tile scan over all problems.
 //  * Offsets mode (the expert-sorted layout of torch.nn.functional.grouped_mm: A [rows, K] and
@@ -680,8 +680,6 @@ grouped_gemm_kernel(KParams p) {
   int* s_tot = s_pref + T::PREFIX + 1;
 
   const int grid = gridDim.x;
-  int vid = blockIdx.x;
-  if ((grid & 7) == 0) vid = (blockIdx.x & 7) * (grid >> 3) + (blockIdx.x >> 3);
 
   int chunk_first = 0;
   const bool searched = p.mode == MODE_GENERIC || p.mode == MODE_OFFSETS;
@@ -694,7 +692,24 @@ grouped_gemm_kernel(KParams p) {
   __shared__ int s_next[2];  // unit broadcast, alternating slots so a slow reader never sees the next
   int parity = 0;
   TileQueue tq{};
-  int u = vid;
+  // Static schedule.  When the grid is a multiple of 8, workgroup b runs on XCD b % 8 (round-robin
+  // dispatch).  With an exact unit count, XCD x owns the contiguous unit range
+  // [x * units / 8, (x + 1) * units / 8), which its grid / 8 workgroups walk with stride grid / 8:
+  // every tile of an expert (both M tiles of a B panel, whatever GROUP_M) is computed on one XCD, so
+  // its B panel is fetched into one L2.  Offsets mode only knows an upper bound of its tiles on the
+  // host, so there each round of grid units is split into eight contiguous runs instead (units past
+  // the device total are spread over all XCDs).  Otherwise workgroup b takes units b, b + grid, ...
+  int u = blockIdx.x, u_step = grid, u_end = units;
+  if ((grid & 7) == 0) {
+    const int xcd = (int)blockIdx.x & 7, per = grid >> 3;
+    if (p.mode == MODE_OFFSETS) {
+      u = xcd * per + (int)(blockIdx.x >> 3);
+    } else {
+      u = (int)((int64_t)xcd * units / 8) + (int)(blockIdx.x >> 3);
+      u_step = per;
+      u_end = (int)((int64_t)(xcd + 1) * units / 8);
+    }
+  }
   // Wave 0 claims the next unit (-1: none left) and the workgroup takes it from LDS.
   auto next_unit = [&](int ticket) {
     if (threadIdx.x < 64) {
@@ -715,7 +730,7 @@ grouped_gemm_kernel(KParams p) {
     u = tq.lo(tq.cur) + (int)blockIdx.x / tq.nx;
     if (u >= tq.lo(tq.cur + 1)) next_unit(-1);  // this XCD has fewer units than workgroups
   }
-  while (stealing ? u >= 0 : u < units) {
+  while (stealing ? u >= 0 : u < u_end) {
     const int t = u % p.total_tiles;
     ProblemDesc pd;
     int tm, tn;
@@ -789,7 +804,7 @@ grouped_gemm_kernel(KParams p) {
     if (stealing)
       next_unit(ticket);
     else
-      u += grid;
+      u += u_step;
   }
   if (stealing && threadIdx.x == 0 && atomicAdd(p.queue + kQueues, 1) == grid - 1) {
     for (int y = 0; y < kQueues; ++y) atomicExch(p.queue + y, 0);

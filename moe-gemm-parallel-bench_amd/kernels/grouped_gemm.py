@@ -392,6 +392,13 @@ def _launch_grouped_fixed(workspace: GroupedWorkspace, cfg: KernelConfig, dtype_
 _GROUPED_AUTOTUNE_CACHE: dict[tuple, tuple] = {}
 
 
+def _grouped_tuning_key(workspace: GroupedWorkspace, scheduler: str, dtype_code: int, precision: int, split_k,
+                        tile_schedule) -> tuple:
+    return (scheduler, workspace.problem_count, workspace.max_m, workspace.max_n, workspace.max_k,
+            workspace.shape_signature, workspace.device_signature, workspace.sm_count, dtype_code, precision,
+            split_k, tile_schedule)
+
+
 def launch_grouped(
     workspace: GroupedWorkspace,
     input_precision: str = "ieee",
@@ -431,11 +438,7 @@ def launch_grouped(
     precision = _native.precision_code(input_precision, dtype_code)
     scheduler = "homogeneous_persistent" if workspace.homogeneous else "generic_persistent"
     if autotune:
-        key = (
-            scheduler, workspace.problem_count, workspace.max_m, workspace.max_n, workspace.max_k,
-            workspace.shape_signature, workspace.device_signature, workspace.sm_count, dtype_code, precision,
-            split_k, tile_schedule,
-        )
+        key = _grouped_tuning_key(workspace, scheduler, dtype_code, precision, split_k, tile_schedule)
         tuned = _GROUPED_AUTOTUNE_CACHE.get(key)
         if tuned is None:
             candidates = grouped_candidate_configs(
@@ -552,7 +555,16 @@ def launch_gate_up_swiglu(
                workspace.shape_signature, workspace.device_signature, workspace.sm_count, dtype_code)
         cfg = _SWIGLU_AUTOTUNE_CACHE.get(key)
         if cfg is None:
-            cfg = _tune(swiglu_candidate_configs(workspace), lambda c: _launch_swiglu_fixed(workspace, c, dtype_code))
+            # The plain W13 GEMM of the same workload, if already tuned, is the preferred tile: the
+            # activation changes only the epilogue, so a different pick would be timing noise.
+            scheduler = "homogeneous_persistent" if workspace.homogeneous else "generic_persistent"
+            plain = _GROUPED_AUTOTUNE_CACHE.get(_grouped_tuning_key(
+                workspace, scheduler, dtype_code, _native.PRECISION_IEEE, None, None))
+            candidates = list(swiglu_candidate_configs(workspace))
+            prefer = plain[0] if plain is not None and plain[0].tile_key in _native.swiglu_tiles(dtype_code) else None
+            if prefer is not None and prefer not in candidates:
+                candidates.append(prefer)
+            cfg = _tune(candidates, lambda c: _launch_swiglu_fixed(workspace, c, dtype_code), prefer=prefer)
             _SWIGLU_AUTOTUNE_CACHE[key] = cfg
     elif cfg is None:
         cfg = swiglu_candidate_configs(workspace)[0]

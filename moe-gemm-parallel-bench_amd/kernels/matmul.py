@@ -416,11 +416,15 @@ def _warm_clocks(launch, budget_ms: float = 100.0) -> None:
 _FINALISTS = 5
 
 
-def _tune(candidates, launch):
+def _tune(candidates, launch, prefer=None, prefer_margin: float = 0.03):
     """Hot-time every candidate (graph replays, bounded) after a clock warm-up, then re-time the best
     five interleaved (three rounds of A, B, C, D, E) and keep the lowest median, so a clock drift
     during tuning shifts every finalist alike instead of favouring whichever ran at the better
-    moment, and a candidate that a noisy first pass ranked fourth or fifth still competes."""
+    moment, and a candidate that a noisy first pass ranked fourth or fifth still competes.
+
+    ``prefer`` (one of the candidates) always joins the finalists and is kept unless another
+    finalist is faster by more than ``prefer_margin``: a choice already measured on the same
+    workload is not overturned by timing noise."""
     candidates = list(candidates)
     measured = []
     warmed = False
@@ -437,9 +441,14 @@ def _tune(candidates, launch):
         raise RuntimeError("every autotune candidate failed to launch")
     measured.sort(key=lambda item: item[0])
     finalists = [cfg for _, cfg in measured[:_FINALISTS]]
+    if prefer is not None and prefer not in finalists and any(cfg == prefer for _, cfg in measured):
+        finalists.append(prefer)
     rounds: list[list[float]] = [[] for _ in finalists]
     for _ in range(3):
         for index, cfg in enumerate(finalists):
             rounds[index].append(hot_autotune_bench(lambda cfg=cfg: launch(cfg), (0.5,))[0])
     medians = [sorted(times)[1] for times in rounds]
-    return finalists[medians.index(min(medians))]
+    best = finalists[medians.index(min(medians))]
+    if prefer in finalists and medians[finalists.index(prefer)] <= min(medians) * (1.0 + prefer_margin):
+        return prefer
+    return best

@@ -193,3 +193,46 @@ def test_validation_errors():
         grouped_mm(a, b[:, :8], torch.tensor([4, 8], device="cuda", dtype=torch.int32))
     with pytest.raises(ValueError):
         grouped_mm(a.t(), b, torch.tensor([4, 8], device="cuda", dtype=torch.int32))
+
+
+def _lognormal_rows(seed: int, groups: int = 32, mean: int = 512, sigma: float = 0.6) -> list[int]:
+    """Ragged routing: lognormal rows per expert around `mean`, with one empty and one single-row expert."""
+    rng = np.random.default_rng(seed)
+    sizes = [int(round(v)) for v in np.exp(rng.normal(math.log(mean) - sigma * sigma / 2, sigma, size=groups))]
+    sizes[5], sizes[9] = 0, 1
+    return sizes
+
+
+@pytest.mark.parametrize("schedule", ["static", "stealing"])
+def test_dsv3_lognormal_routing_exact_and_oracle(schedule):
+    """DSV3 EP W13 shard (32 experts, K = 7168, N = 4096) with lognormal routing: exact integers on
+    every expert and oracle tail rows of the first and last non-empty experts, under each tile
+    schedule with the autotuned config of that schedule."""
+    from kernels.grouped_mm import grouped_mm
+
+    sizes = _lognormal_rows(2024)
+    offs_list = list(np.cumsum(sizes))
+    rows, k, n, groups = offs_list[-1], 7168, 4096, len(sizes)
+    print(f"offsets DSV3 lognormal schedule={schedule} rows={rows} sizes={sizes}", flush=True)
+    offs = torch.tensor(offs_list, device="cuda", dtype=torch.int32)
+    mat_a, mat_b = _operands(rows, k, n, groups, torch.bfloat16)
+    out = torch.full((rows, n), float("nan"), device="cuda", dtype=torch.bfloat16)
+    grouped_mm(mat_a, mat_b, offs, out=out, tile_schedule=schedule)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    nonempty = [e for e, m in enumerate(sizes) if m]
+    for e in (nonempty[0], nonempty[-1]):
+        r1 = offs_list[e]
+        tail = slice(max(r1 - 3, r1 - sizes[e]), r1)
+        expected = from_oracle(oracle.gemm(to_oracle(mat_a[tail]), to_oracle(mat_b[e]), "bf16"), "bf16")
+        assert normwise(out[tail].cpu(), expected) <= 1e-2, f"expert {e}"
+    mat_a.fill_(1)
+    for e in range(groups):
+        mat_b[e].fill_(e % 31 + 1)
+    out.fill_(float("nan"))
+    grouped_mm(mat_a, mat_b, offs, out=out, tile_schedule=schedule)
+    torch.cuda.synchronize()
+    for e in range(groups):
+        r0, r1 = (offs_list[e - 1] if e else 0), offs_list[e]
+        if r1 > r0:
+            assert torch.equal(out[r0:r1], torch.full_like(out[r0:r1], float(k * (e % 31 + 1)))), f"expert {e}"
