@@ -21,11 +21,12 @@
 //  * Fragment reads for K step kk+1 are issued before the MFMAs of step kk (register double
 //    buffering) so the MFMA pipe does not wait on LDS latency inside a slice.
 //  * SwiGLU epilogue (packed W13, B = [gate | up] with n = 2F columns): a tile of output columns
-//    [n0/2, n0/2 + BN/2) loads, into the first half of every wave's WTN-column block, the gate
-//    columns and, into the second half, the matching up columns (F + the same offsets).  Fragment
-//    fn and fn + FN/2 of a lane then cover the same output columns, so the epilogue forms
-//    silu(gate) * up from the fp32 accumulators in registers and stores F-wide rows.  Needs an
-//    even FN and F a multiple of 8 (checked by the host).
+//    [n0/2, n0/2 + BN/2) loads the gate columns into the first half of the LDS B row and the
+//    matching up columns (F further on) into the second half, so every B row is read as two
+//    contiguous runs.  A wave's fragments fn < FN/2 read its WTN/2 gate columns and fragments
+//    fn + FN/2 the same output columns' up values, so the epilogue forms silu(gate) * up from the
+//    fp32 accumulators in registers and stores F-wide rows.  Needs an even FN and F a multiple of 8
+//    (checked by the host).
 //  * Split-K units (KParams::splits > 1) end with split_store instead of the C store: the fp32
 //    partial tile goes to the caller's workspace with device-coherent (sc1) 16-byte stores, the
 //    workgroup waits for them to complete before one atomic increment of the tile's counter, and
@@ -193,10 +194,12 @@ struct FastTile {
       const int pc = lane % CB;
       const int c = pc ^ swz_b(r, CB);
       if (pd.swiglu) {
-        // Logical chunk c of the tile: wave block c / CPW; its first half gate, second half up.
-        const int f = pd.n >> 1, half = CPW / 2, cc = c % CPW;
-        const int ocol = (n0 >> 1) + (c / CPW) * (WTN / 2) + (cc % half) * 8;
-        const int gcol = cc < half ? ocol : f + ocol;
+        // Logical chunk c of the tile: the first half of the row holds the gate columns of output
+        // columns [n0/2, n0/2 + BN/2), the second half the matching up columns (F further on), so
+        // each B row is read as two contiguous BN-byte runs.
+        const int f = pd.n >> 1, half = CB / 2;
+        const int ocol = (n0 >> 1) + (c % half) * 8;
+        const int gcol = c < half ? ocol : f + ocol;
         d.b_off[q] = ocol < f ? (uint32_t)r * d.ldb_bytes + (uint32_t)gcol * 2u : kOutOfRange;
       } else {
         d.b_off[q] = (n0 + c * 8 < pd.n) ? (uint32_t)r * d.ldb_bytes + (uint32_t)c * 16u : kOutOfRange;
@@ -228,8 +231,17 @@ struct FastTile {
     }
   }
 
+  // First LDS column of B fragment fn: the wave's WTN-column block, or under the SwiGLU layout the
+  // wave's WTN/2 gate columns (fragments fn < FN/2) and, BN/2 further on, the matching up columns.
+  __device__ static __forceinline__ int b_frag_col(int fn, int wave_n, bool swiglu) {
+    if (SWIGLU_OK && swiglu)
+      return (fn < FN / 2 ? 0 : BN / 2) + wave_n * (WTN / 2) + (fn % (FN / 2 > 0 ? FN / 2 : 1)) * MI;
+    return wave_n * WTN + fn * MI;
+  }
+
   __device__ static __forceinline__ void load_frags(i16x8_t (&af)[FM], i16x8_t (&bf)[FN], const char* lds_a,
-                                                    const char* lds_b, int kk, int wave_m, int wave_n) {
+                                                    const char* lds_b, int kk, int wave_m, int wave_n,
+                                                    bool swiglu = false) {
     const int lane = threadIdx.x & 63;
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
@@ -244,10 +256,10 @@ struct FastTile {
       int row, col;
       if constexpr (MI == 32) {
         row = kk * MIK + 8 * (g >> 1) + (s >> 2);
-        col = wave_n * WTN + fn * 32 + 16 * (g & 1) + 4 * (s & 3);
+        col = b_frag_col(fn, wave_n, swiglu) + 16 * (g & 1) + 4 * (s & 3);
       } else {
         row = kk * MIK + 8 * g + (s >> 2);
-        col = wave_n * WTN + fn * 16 + 4 * (s & 3);
+        col = b_frag_col(fn, wave_n, swiglu) + 4 * (s & 3);
       }
       const int pc = (col >> 3) ^ swz_b(row, CB);
       const char* p0 = lds_b + (row * CB + pc) * 16 + (col & 7) * 2;
@@ -599,7 +611,7 @@ struct FastTile {
     __builtin_amdgcn_s_barrier();
     compiler_fence();
     i16x8_t af[2][FM], bf[2][FN];
-    load_frags(af[0], bf[0], smem, smem + A_BYTES, 0, wave_m, wave_n);
+    load_frags(af[0], bf[0], smem, smem + A_BYTES, 0, wave_m, wave_n, pd.swiglu != 0);
 
     const int kt_count = (pd.k + BK - 1) / BK;
     for (int kt = 0; kt < kt_count; ++kt) {
@@ -607,7 +619,8 @@ struct FastTile {
       const char* nxt = smem + ((kt + 1) % STAGES) * STAGE_BYTES;
 #pragma unroll
       for (int kk = 0; kk < KK - 1; ++kk) {
-        load_frags(af[(kk + 1) & 1], bf[(kk + 1) & 1], cur, cur + A_BYTES, kk + 1, wave_m, wave_n);
+        load_frags(af[(kk + 1) & 1], bf[(kk + 1) & 1], cur, cur + A_BYTES, kk + 1, wave_m, wave_n,
+                   pd.swiglu != 0);
         mfma_rows<0, FM>(acc, af[kk & 1], bf[kk & 1]);
         interleave<FM * FN, NDS, 0>();
       }
@@ -622,7 +635,7 @@ struct FastTile {
       __builtin_amdgcn_s_barrier();
       compiler_fence();
       issue_stage(d, kt % STAGES, (kt + STAGES) * BK);
-      load_frags(af[0], bf[0], nxt, nxt + A_BYTES, 0, wave_m, wave_n);
+      load_frags(af[0], bf[0], nxt, nxt + A_BYTES, 0, wave_m, wave_n, pd.swiglu != 0);
       mfma_rows<HALF, FM>(acc, af[L], bf[L]);
       interleave<(FM - HALF) * FN, NDS, NVM>();
     }

@@ -84,7 +84,8 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
       const char* cur = smem + (kt % STAGES) * STAGE_BYTES;
       if (kt >= 1) Base::issue_stage(d, (kt - 1) % STAGES, (kt - 1 + STAGES) * BK);
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) Base::load_frags(af[kk], bf[kk], cur, cur + A_BYTES, kk, wave_m, wave_n);
+      for (int kk = 0; kk < KK; ++kk)
+        Base::load_frags(af[kk], bf[kk], cur, cur + A_BYTES, kk, wave_m, wave_n, pd.swiglu != 0);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       if (second) wait_vmcnt<(STAGES - 2) * XMIN>();
       phase_barrier();
