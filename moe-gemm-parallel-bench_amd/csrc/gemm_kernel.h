@@ -685,24 +685,28 @@ grouped_gemm_kernel(KParams p) {
   const bool searched = p.mode == MODE_GENERIC || p.mode == MODE_OFFSETS;
   if (searched) load_prefix<T>(p, s_pref, s_tot, 0, 0);
 
-  // Units: tile t, K split u / total_tiles (one split outside split-K launches).
+  // Units: tile t, K split u / total_tiles (one split outside split-K launches).  Generic and
+  // offsets launches whose groups fit one prefix chunk know their exact tile count on the device
+  // (offsets mode gets only an upper bound from the host): the schedules partition that.
   const int splits = p.splits > 1 ? p.splits : 1;
-  const int units = p.total_tiles * splits;
+  int units = p.total_tiles * splits;
+  if (searched && p.G <= T::PREFIX) units = min(units, s_pref[T::PREFIX] * splits);
   const bool stealing = p.queue != nullptr;
   __shared__ int s_next[2];  // unit broadcast, alternating slots so a slow reader never sees the next
   int parity = 0;
   TileQueue tq{};
   // Static schedule.  When the grid is a multiple of 8, workgroup b runs on XCD b % 8 (round-robin
-  // dispatch).  With an exact unit count, XCD x owns the contiguous unit range
-  // [x * units / 8, (x + 1) * units / 8), which its grid / 8 workgroups walk with stride grid / 8:
-  // every tile of an expert (both M tiles of a B panel, whatever GROUP_M) is computed on one XCD, so
-  // its B panel is fetched into one L2.  Offsets mode only knows an upper bound of its tiles on the
-  // host, so there each round of grid units is split into eight contiguous runs instead (units past
-  // the device total are spread over all XCDs).  Otherwise workgroup b takes units b, b + grid, ...
+  // dispatch).  Single and homogeneous launches (tiles of equal cost): XCD x owns the contiguous
+  // unit range [x * units / 8, (x + 1) * units / 8), which its grid / 8 workgroups walk with stride
+  // grid / 8, so every tile of an expert (both M tiles of a B panel, whatever GROUP_M) is computed
+  // on one XCD and its B panel is fetched into one L2.  Generic and offsets launches (tiles of
+  // unequal cost: ragged groups, partial M tiles) split each round of grid units into eight
+  // contiguous runs instead, which spreads every part of the tile space over all XCDs.  Otherwise
+  // workgroup b takes units b, b + grid, ...
   int u = blockIdx.x, u_step = grid, u_end = units;
   if ((grid & 7) == 0) {
     const int xcd = (int)blockIdx.x & 7, per = grid >> 3;
-    if (p.mode == MODE_OFFSETS) {
+    if (searched) {
       u = xcd * per + (int)(blockIdx.x >> 3);
     } else {
       u = (int)((int64_t)xcd * units / 8) + (int)(blockIdx.x >> 3);
