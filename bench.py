@@ -6,7 +6,11 @@
   [512, 7168] @ [7168, 4096] in bf16 with fp32 accumulation, synthetic ``normal_() * 0.1`` inputs
   resident in HBM.  A step is one ``launch_grouped`` call over the whole group (one kernel launch).
 * ``value`` is whole-job TFLOP/s = 2 * sum_e M_e*K*N / (time per step), from HIP events recorded on
-  the launch stream around exactly K back-to-back steps (synchronised before and after).
+  the launch stream around exactly K back-to-back steps (synchronised before and after).  Before
+  the W warmup steps the step runs back to back for ``--settle-seconds`` (3 s): at its 1400 W cap
+  the GPU boosts, then throttles below its steady clock for about a second of sustained load, and
+  K steps timed straight after an idle period measure that transient.  ``cold_ms_per_step`` is
+  the same K steps timed without the settle period, reported beside it.
 * ``roofline`` prices that kernel against the dense bf16 MFMA peak (2.5 PFLOP/s); ``traffic`` is
   the measured HBM bytes per launch from profiles/ (rocprofv3 FETCH_SIZE + WRITE_SIZE, scaled by a
   copy-kernel calibration) or null when no such profile is committed.
@@ -72,15 +76,36 @@ def _check_sample(workspace, experts=(0, -1)) -> float:
     return worst
 
 
-def _time_steps(workspace, steps: int, warmup: int, pinned) -> tuple[float, float]:
-    """(ms per step from HIP events on the launch stream, wall ms per step)."""
+def _settle(step, seconds: float) -> None:
+    """Run ``step`` back to back for ``seconds`` (untimed), keeping the queue non-empty.
+
+    An MI355X held at its board power cap boosts at the start of a sustained load, then throttles
+    past its steady clock and takes one to two seconds to settle (kernel traces show single
+    dispatches of the headline 45 % slower than the steady state a few launches in); steps timed
+    right after an idle period measure that transient rather than the sustained rate."""
     import torch
 
-    from kernels.grouped_gemm import launch_grouped
+    if seconds <= 0:
+        return
+    deadline = time.perf_counter() + seconds
+    previous = None
+    while time.perf_counter() < deadline:
+        for _ in range(8):
+            step()
+        event = torch.cuda.Event()
+        event.record(torch.cuda.current_stream())
+        if previous is not None:
+            previous.synchronize()
+        previous = event
+    torch.cuda.synchronize()
 
-    def step():
-        launch_grouped(workspace, config=pinned, autotune=pinned is None)
 
+def _timed(step, steps: int, warmup: int, settle_s: float = 0.0) -> tuple[float, float]:
+    """(ms per step from HIP events on the launch stream, wall ms per step) over exactly ``steps``
+    back-to-back steps, after the settle period and ``warmup`` untimed steps."""
+    import torch
+
+    _settle(step, settle_s)
     for _ in range(warmup):
         step()
     stream = torch.cuda.current_stream()
@@ -98,7 +123,7 @@ def _time_steps(workspace, steps: int, warmup: int, pinned) -> tuple[float, floa
 
 
 def _case(projection: str, parallel_type: str, m: int, steps: int, warmup: int, seed: int = 1234,
-          pinned=None, model: str = "dsv3") -> dict:
+          pinned=None, model: str = "dsv3", settle_s: float = 0.0) -> dict:
     """Time one case of a BASELINE model (DSV3 by default); ``pinned`` (a KernelConfig) skips autotuning."""
     import torch
 
@@ -112,13 +137,17 @@ def _case(projection: str, parallel_type: str, m: int, steps: int, warmup: int, 
     launch_grouped(workspace, config=pinned, autotune=pinned is None)
     torch.cuda.synchronize()
     error = _check_sample(workspace)
-    ms, wall_ms = _time_steps(workspace, steps, warmup, pinned)
+
+    def step():
+        launch_grouped(workspace, config=pinned, autotune=pinned is None)
+
+    cold_ms, _ = _timed(step, steps, warmup)  # straight after the idle check, no settle period
+    ms, wall_ms = _timed(step, steps, warmup, settle_s)
     # Device time per launch from hipGraph replays (the reference's timing method): for kernels
     # shorter than the Python launch path the eager loop above measures the host, not the kernel.
     from utils.benchmark import time_cuda
 
-    graph_ms = time_cuda(lambda _i: launch_grouped(workspace, config=pinned, autotune=pinned is None),
-                         warmup, max(steps, 20), 200.0).median_ms
+    graph_ms = time_cuda(lambda _i: step(), warmup, max(steps, 20), 200.0).median_ms
     flops = sum(gemm_flops(*s) for s in workspace.shapes)
     nbytes = sum(gemm_bytes(*s, 2) for s in workspace.shapes)
     tflops = flops / (ms * 1e9)
@@ -127,7 +156,8 @@ def _case(projection: str, parallel_type: str, m: int, steps: int, warmup: int, 
     row = {
         "case": f"{model}_{projection.lower()}_{parallel_type.lower()}_me{m}",
         "experts": workspace.problem_count, "shape_mkn": list(workspace.shapes[0]),
-        "ms": ms, "wall_ms": wall_ms, "graph_ms": graph_ms, "tflops": tflops, "gbs": gbs, "bound": bound,
+        "ms": ms, "wall_ms": wall_ms, "cold_ms": cold_ms, "graph_ms": graph_ms, "settle_s": settle_s,
+        "tflops": tflops, "gbs": gbs, "bound": bound,
         "frac": tflops / PEAK_BF16_TFLOPS if bound == "mfma" else gbs / PEAK_HBM_GBS,
         "config": workspace.config.as_dict(), "scheduler": workspace.scheduler,
         "tile_schedule": workspace.tile_schedule, "split_k": workspace.split_k,
@@ -139,7 +169,7 @@ def _case(projection: str, parallel_type: str, m: int, steps: int, warmup: int, 
     return row
 
 
-def _swiglu_case(m: int, steps: int, warmup: int, seed: int = 1234) -> dict:
+def _swiglu_case(m: int, steps: int, warmup: int, seed: int = 1234, settle_s: float = 0.0) -> dict:
     """DSV3 EP W13 with the SwiGLU activation fused into the epilogue (labelled variant)."""
     import torch
 
@@ -161,27 +191,21 @@ def _swiglu_case(m: int, steps: int, warmup: int, seed: int = 1234) -> dict:
     from kernels.grouped_gemm import launch_grouped
 
     cfg = workspace.swiglu_config
-    stream = torch.cuda.current_stream()
 
-    def timed(step) -> float:
-        for _ in range(warmup):
-            step()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        start.record(stream)
-        for _ in range(steps):
-            step()
-        end.record(stream)
-        torch.cuda.synchronize()
-        return start.elapsed_time(end) / steps
+    def fused_step():
+        launch_gate_up_swiglu(workspace)
 
-    # SwiGLU and the plain W13 GEMM with the same tile, interleaved (three rounds each), so the gap
-    # is measured under one clock state rather than against a case timed minutes earlier.
+    def plain_step():
+        launch_grouped(workspace, config=cfg, autotune=False, split_k=1, tile_schedule="static")
+
+    # SwiGLU and the plain W13 GEMM with the same tile, interleaved (three rounds each) after one
+    # settle period, so the gap is measured under one clock state rather than against a case timed
+    # minutes earlier.
+    _settle(fused_step, settle_s)
     fused, plain = [], []
     for _ in range(3):
-        fused.append(timed(lambda: launch_gate_up_swiglu(workspace)))
-        plain.append(timed(lambda: launch_grouped(workspace, config=cfg, autotune=False, split_k=1,
-                                                  tile_schedule="static")))
+        fused.append(_timed(fused_step, steps, warmup)[0])
+        plain.append(_timed(plain_step, steps, warmup)[0])
     ms, plain_ms = sorted(fused)[1], sorted(plain)[1]
     flops = sum(gemm_flops(*s) for s in workspace.shapes)
     nbytes = sum(2 * (mm * k + k * n + mm * n // 2) for mm, k, n in workspace.shapes)
@@ -199,7 +223,7 @@ def _swiglu_case(m: int, steps: int, warmup: int, seed: int = 1234) -> dict:
     return row
 
 
-def _ragged_case(steps: int, warmup: int, seed: int = 1234) -> dict:
+def _ragged_case(steps: int, warmup: int, seed: int = 1234, settle_s: float = 0.0) -> dict:
     """DSV3 EP W13 over the expert-sorted layout with lognormal routing (32 experts, rows around
     512, one empty and one single-row expert): each tile schedule timed with its own tuned config."""
     import math
@@ -219,24 +243,23 @@ def _ragged_case(steps: int, warmup: int, seed: int = 1234) -> dict:
     flops = sum(gemm_flops(m, k, n) for m in sizes)
     row = {"case": "dsv3_w1_ep_lognormal_offsets", "experts": len(sizes), "rows": sum(sizes),
            "rows_min_max": [min(sizes), max(sizes)], "flops": flops, "schedules": {}}
-    stream = torch.cuda.current_stream()
+    steps_by_schedule = {}
     for schedule in ("static", "stealing"):
-        def step():
+        def step(schedule=schedule):
             grouped_mm(ws.mat_a, ws.mat_b, ws.offs, out=ws.output, tile_schedule=schedule)
 
         step()  # autotune (untimed) for this schedule
-        for _ in range(warmup):
-            step()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        start.record(stream)
-        for _ in range(steps):
-            step()
-        end.record(stream)
-        torch.cuda.synchronize()
-        ms = start.elapsed_time(end) / steps
-        row["schedules"][schedule] = {"ms": ms, "tflops": flops / (ms * 1e9),
-                                      "config": last_grouped_mm_config().as_dict()}
+        steps_by_schedule[schedule] = (step, last_grouped_mm_config().as_dict())
+    # One settle period, then the schedules interleaved (three rounds each, median), so both see
+    # the same clock state.
+    _settle(steps_by_schedule["static"][0], settle_s)
+    rounds = {schedule: [] for schedule in steps_by_schedule}
+    for _ in range(3):
+        for schedule, (step, _) in steps_by_schedule.items():
+            rounds[schedule].append(_timed(step, steps, warmup)[0])
+    for schedule, (_, config) in steps_by_schedule.items():
+        ms = sorted(rounds[schedule])[1]
+        row["schedules"][schedule] = {"ms": ms, "tflops": flops / (ms * 1e9), "config": config}
     worst = 0.0
     begin = 0
     for e, m in enumerate(sizes):
@@ -382,11 +405,20 @@ def _cpu_oracle_port(seconds_target: float = 5.0) -> dict:
     }
 
 
+def _progress(row: dict) -> dict:
+    """One line per finished case on stderr (stdout carries only the JSON result line)."""
+    print(f"bench: {row['case']} {row['ms'] * 1e3:.1f} us per step", file=sys.stderr, flush=True)
+    return row
+
+
 def main(argv=None) -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--settle-seconds", type=float, default=3.0,
+                        help="untimed back-to-back steps before the warmup steps, so the timed steps see "
+                             "the power manager's steady state (the cases use half); 0 disables")
     parser.add_argument("--no-cases", action="store_true", help="only the headline case")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--kernel-config", metavar="BM,BN,BK,WARPS,STAGES,GROUP_M,MULT", default=None,
@@ -402,8 +434,8 @@ def main(argv=None) -> int:
         print("bench.py measures one MI355X: this build has no multi-GPU path (every GPU box here has "
               "one GPU); run with --gpus 1.", file=sys.stderr)
         return 2
-    if args.steps < 1 or args.warmup < 0:
-        raise SystemExit("--steps must be >= 1 and --warmup >= 0")
+    if args.steps < 1 or args.warmup < 0 or args.settle_seconds < 0:
+        raise SystemExit("--steps must be >= 1, --warmup and --settle-seconds >= 0")
     import torch
 
     if not torch.cuda.is_available():
@@ -427,18 +459,22 @@ def main(argv=None) -> int:
         projection, parallel_type, m = args.case.split(",")
         if projection not in ("W1", "W2") or parallel_type not in ("EP", "TP"):
             raise SystemExit("--case takes PROJ,PAR,M with PROJ in W1/W2 and PAR in EP/TP")
-        row = _case(projection, parallel_type, int(m), args.steps, args.warmup, pinned=pinned, model=args.model)
+        row = _case(projection, parallel_type, int(m), args.steps, args.warmup, pinned=pinned, model=args.model,
+                    settle_s=args.settle_seconds)
         print(json.dumps(row))
         return 0 if row["correct"] else 1
-    headline = _case("W1", "EP", 512, args.steps, args.warmup, pinned=pinned)
+    headline = _case("W1", "EP", 512, args.steps, args.warmup, pinned=pinned, settle_s=args.settle_seconds)
+    _progress(headline)
+    case_settle = args.settle_seconds / 2
     cases = []
     if not args.no_cases:
         for projection, parallel_type, m in (("W1", "EP", 8), ("W1", "TP", 512), ("W1", "TP", 8),
                                             ("W2", "EP", 512), ("W2", "TP", 512), ("W2", "EP", 8),
                                             ("W2", "TP", 8)):
-            cases.append(_case(projection, parallel_type, m, max(5, args.steps // 2), 2))
-        cases.append(_swiglu_case(512, max(5, args.steps // 2), 2))
-        cases.append(_ragged_case(max(5, args.steps // 2), 2))
+            cases.append(_progress(_case(projection, parallel_type, m, max(5, args.steps // 2), 2,
+                                         settle_s=case_settle)))
+        cases.append(_progress(_swiglu_case(512, max(5, args.steps // 2), 2, settle_s=case_settle)))
+        cases.append(_progress(_ragged_case(max(5, args.steps // 2), 2, settle_s=case_settle)))
     traffic = _traffic_from_profiles(headline["case"])
     tp = next((c for c in cases if c["case"] == "dsv3_w1_tp_me512"), None)
     by_case = {c["case"]: c for c in cases + [headline]}
@@ -457,6 +493,8 @@ def main(argv=None) -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": headline["ms"],
+        "settle_s": args.settle_seconds,
+        "cold_ms_per_step": headline["cold_ms"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -508,7 +508,7 @@ struct FastTile {
       if (gm < pd.m && gn < pd.n) {
         char* dst = pd.c + ((int64_t)gm * pd.scm + gn) * 2;
         if (c16) {
-          *MOEGEMM_GLOBAL(u32x4_t, dst) = v;
+          __builtin_nontemporal_store(v, MOEGEMM_GLOBAL(u32x4_t, dst));  // non-temporal, as store4
         } else {
           *MOEGEMM_GLOBAL(u32x2_t, dst) = u32x2_t{v[0], v[1]};
           *MOEGEMM_GLOBAL(u32x2_t, dst + 8) = u32x2_t{v[2], v[3]};
