@@ -156,11 +156,8 @@ __device__ __forceinline__ uint32_t tf32_round(uint32_t u) {
   return (u + 0x1000u) & 0xffffe000u;
 }
 
-// Four fp32 results converted to the output type and stored (8 or 16 bytes).  16-bit outputs are
-// written once and never re-read by the launch, so they go out as non-temporal stores: they stream
-// through L2 instead of evicting the A and B panels that other workgroups of the XCD are about to
-// re-read (DSV3 TP W2, M_e = 512, writes 1.9 GB of C per launch; its measured HBM fetch fell from
-// 1.88 to 1.37 GB with these stores).
+// Four fp32 results converted to the output type and stored (8 or 16 bytes).  These stores cover
+// part of a cache line; L2 merges the neighbouring pieces before the line goes out.
 template <class E>
 __device__ __forceinline__ void store4(char* dst, f32x4_t v);
 
@@ -170,14 +167,14 @@ __device__ __forceinline__ void store4<EBf16>(char* dst, f32x4_t v) {
   typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
   bf16x4_t o;
   o[0] = (__bf16)v[0]; o[1] = (__bf16)v[1]; o[2] = (__bf16)v[2]; o[3] = (__bf16)v[3];
-  __builtin_nontemporal_store(o, MOEGEMM_GLOBAL(bf16x4_t, dst));
+  *MOEGEMM_GLOBAL(bf16x4_t, dst) = o;
 }
 template <>
 __device__ __forceinline__ void store4<EF16>(char* dst, f32x4_t v) {
   typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
   f16x4_t o;
   o[0] = (_Float16)v[0]; o[1] = (_Float16)v[1]; o[2] = (_Float16)v[2]; o[3] = (_Float16)v[3];
-  __builtin_nontemporal_store(o, MOEGEMM_GLOBAL(f16x4_t, dst));
+  *MOEGEMM_GLOBAL(f16x4_t, dst) = o;
 }
 template <>
 __device__ __forceinline__ void store4<EF32>(char* dst, f32x4_t v) {
