@@ -17,7 +17,8 @@
 * ``cases`` adds the HBM-bound M_e = 8 EP case, the TP counterparts (EP/TP ratio), the DSV3 W2
   cases, the headline with the SwiGLU activation fused into the epilogue (a labelled variant:
   the reference times W13 without the activation) and the headline's work under lognormal routing
-  over the expert-sorted layout, timed under the static and the work-stealing tile schedule; each
+  (rows around 512 and around 64 per expert) over the expert-sorted layout, timed under the static
+  and the work-stealing tile schedule; each
   is timed the same way and checked against a float32 torch reference on a sample of experts.
 * ``cpu_baseline`` times the reference's own CPU torch path for the headline step on the host cores
   (per-expert ``torch.mm`` and ``F.grouped_mm`` over the padded offs layout; the faster is
@@ -223,9 +224,10 @@ def _swiglu_case(m: int, steps: int, warmup: int, seed: int = 1234, settle_s: fl
     return row
 
 
-def _ragged_case(steps: int, warmup: int, seed: int = 1234, settle_s: float = 0.0) -> dict:
+def _ragged_case(steps: int, warmup: int, seed: int = 1234, settle_s: float = 0.0, mean_rows: int = 512) -> dict:
     """DSV3 EP W13 over the expert-sorted layout with lognormal routing (32 experts, rows around
-    512, one empty and one single-row expert): each tile schedule timed with its own tuned config."""
+    ``mean_rows``, one empty and one single-row expert): each tile schedule timed with its own tuned
+    config."""
     import math
 
     import numpy as np
@@ -236,12 +238,13 @@ def _ragged_case(steps: int, warmup: int, seed: int = 1234, settle_s: float = 0.
 
     rng = np.random.default_rng(2024)
     sigma = 0.6
-    sizes = [int(round(v)) for v in np.exp(rng.normal(math.log(512) - sigma * sigma / 2, sigma, size=32))]
+    sizes = [int(round(v)) for v in np.exp(rng.normal(math.log(mean_rows) - sigma * sigma / 2, sigma, size=32))]
     sizes[5], sizes[9] = 0, 1
     k, n = DSV3["hidden"], 2 * DSV3["ffn"]
     ws = build_offsets_workspace([(m, k, n) for m in sizes], torch.bfloat16, seed, operation="gate_up")
     flops = sum(gemm_flops(m, k, n) for m in sizes)
-    row = {"case": "dsv3_w1_ep_lognormal_offsets", "experts": len(sizes), "rows": sum(sizes),
+    name = "dsv3_w1_ep_lognormal_offsets" if mean_rows == 512 else f"dsv3_w1_ep_lognormal{mean_rows}_offsets"
+    row = {"case": name, "experts": len(sizes), "rows": sum(sizes),
            "rows_min_max": [min(sizes), max(sizes)], "flops": flops, "schedules": {}}
     steps_by_schedule = {}
     for schedule in ("static", "stealing"):
@@ -474,7 +477,8 @@ def main(argv=None) -> int:
             cases.append(_progress(_case(projection, parallel_type, m, max(5, args.steps // 2), 2,
                                          settle_s=case_settle)))
         cases.append(_progress(_swiglu_case(512, max(5, args.steps // 2), 2, settle_s=case_settle)))
-        cases.append(_progress(_ragged_case(max(5, args.steps // 2), 2, settle_s=case_settle)))
+        for mean_rows in (512, 64):
+            cases.append(_progress(_ragged_case(max(5, args.steps // 2), 2, settle_s=case_settle, mean_rows=mean_rows)))
     traffic = _traffic_from_profiles(headline["case"])
     tp = next((c for c in cases if c["case"] == "dsv3_w1_tp_me512"), None)
     by_case = {c["case"]: c for c in cases + [headline]}

@@ -203,17 +203,18 @@ def _lognormal_rows(seed: int, groups: int = 32, mean: int = 512, sigma: float =
     return sizes
 
 
+@pytest.mark.parametrize("mean", [512, 64])
 @pytest.mark.parametrize("schedule", ["static", "stealing"])
-def test_dsv3_lognormal_routing_exact_and_oracle(schedule):
-    """DSV3 EP W13 shard (32 experts, K = 7168, N = 4096) with lognormal routing: exact integers on
-    every expert and oracle tail rows of the first and last non-empty experts, under each tile
-    schedule with the autotuned config of that schedule."""
+def test_dsv3_lognormal_routing_exact_and_oracle(schedule, mean):
+    """DSV3 EP W13 shard (32 experts, K = 7168, N = 4096) with lognormal routing around `mean` rows:
+    exact integers on every expert and oracle tail rows of the first and last non-empty experts,
+    under each tile schedule with the autotuned config of that schedule."""
     from kernels.grouped_mm import grouped_mm
 
-    sizes = _lognormal_rows(2024)
+    sizes = _lognormal_rows(2024, mean=mean)
     offs_list = list(np.cumsum(sizes))
     rows, k, n, groups = offs_list[-1], 7168, 4096, len(sizes)
-    print(f"offsets DSV3 lognormal schedule={schedule} rows={rows} sizes={sizes}", flush=True)
+    print(f"offsets DSV3 lognormal mean={mean} schedule={schedule} rows={rows} sizes={sizes}", flush=True)
     offs = torch.tensor(offs_list, device="cuda", dtype=torch.int32)
     mat_a, mat_b = _operands(rows, k, n, groups, torch.bfloat16)
     out = torch.full((rows, n), float("nan"), device="cuda", dtype=torch.bfloat16)
