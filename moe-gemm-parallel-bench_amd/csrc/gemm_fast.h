@@ -655,6 +655,149 @@ struct FastTile {
     compiler_fence();
     store_tile(acc, pd, m0, n0, wave_m, wave_n, smem);
   }
+
+  // Cross-tile chaining, for the two-stage tiles whose C leaves by direct stores (the 16-row decode
+  // tiles).  A workgroup on the static schedule knows its next unit.  So the copy that would fill
+  // the drained buffer with a zero slice past K fetches the next tile's slice 0 instead, and the
+  // next tile starts with that slice in flight.  It sits in the buffer after this tile's last one:
+  // buffer roles rotate by the K slice count at every tile.  This tile's C then leaves by buffer
+  // stores issued with every lane active, exactly CHAIN_STORES per wave; out-of-range lanes are
+  // dropped by the range check.  A wave's vector memory operations complete in issue order, so the
+  // next tile knows its slice 0 has landed once at most CHAIN_STORES operations are outstanding.
+  // It does not wait for the stores themselves.
+  static constexpr bool CHAIN_OK = STAGES == 2 && !STAGED_OK;
+  static constexpr int CHAIN_STORES = FM * FN * (ACC / 4);
+  static_assert(!CHAIN_OK || CHAIN_STORES + QA + QB < 64, "outstanding operations must fit the 6-bit vmcnt");
+  struct Chain {
+    Dma d;            // copy state of the tile whose slice 0 the previous tile issued
+    int rot;          // LDS buffer holding that slice 0
+    bool prefetched;  // false: the next tile issues its own prologue
+  };
+
+  // C stores with a fixed instruction count per wave: CHAIN_STORES 8-byte buffer stores.
+  __device__ static __forceinline__ void store_tile_counted(const acc_t (&acc)[FM][FN], const ProblemDesc& pd,
+                                                            int m0, int n0, int wave_m, int wave_n) {
+    const int lane = threadIdx.x & 63;
+    const int rows = min(BM, pd.m - m0);
+    const auto rc = __builtin_amdgcn_make_buffer_rsrc(pd.c + (int64_t)m0 * pd.scm * 2, (short)0,
+                                                      (int)((uint32_t)rows * (uint32_t)pd.scm * 2u), (int)kBufferFlags);
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      const int rl = wave_m * WTM + fm * MI + (lane % MI);
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int q = 0; q < ACC / 4; ++q) {
+          const int nloc = (MI == 32) ? (q * 8 + (lane >> 5) * 4) : ((lane >> 4) * 4);
+          const int gn = n0 + wave_n * WTN + fn * MI + nloc;
+          const uint32_t off =
+              (rl < rows && gn < pd.n) ? ((uint32_t)rl * (uint32_t)pd.scm + (uint32_t)gn) * 2u : kOutOfRange;
+          const f32x4_t v = {acc[fm][fn][q * 4 + 0], acc[fm][fn][q * 4 + 1], acc[fm][fn][q * 4 + 2],
+                             acc[fm][fn][q * 4 + 3]};
+          __builtin_amdgcn_raw_buffer_store_b64(pack4<E>(v), rc, (int)off, 0, 0);
+        }
+    }
+  }
+
+  // run_tile's schedule for CHAIN_OK tiles; `next` is the workgroup's next tile when `has_next`.
+  // `ch` carries the prefetch from one call to the next; start a workgroup with ch.prefetched false.
+  __device__ static __forceinline__ void run_tile_chained(const ProblemDesc& pd, int tm, int tn, char* smem,
+                                                          const ProblemDesc& next, bool has_next, int ntm, int ntn,
+                                                          Chain& ch) {
+    static_assert(CHAIN_OK, "the chained schedule is for two-stage tiles with direct C stores");
+    static_assert(KK % 2 == 0, "fragment double buffer alternates by K step");
+    constexpr int HALF = FM / 2 > 0 ? FM / 2 : 1;
+    constexpr int NDS = FM + 2 * FN;
+    constexpr int NVM = QA + QB;
+    const int wave = threadIdx.x >> 6;
+    const int wave_m = wave / WN, wave_n = wave % WN;
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    acc_t acc[FM][FN];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int i = 0; i < ACC; ++i) acc[fm][fn][i] = 0.0f;
+
+    Dma d;
+    int rot = 0;
+    if (ch.prefetched) {
+      // Slice 0 was issued before the previous tile's CHAIN_STORES stores, with nothing else of
+      // this wave outstanding; the previous tile's LDS reads are done once every wave is here.
+      d = ch.d;
+      rot = ch.rot;
+      wait_vmcnt<CHAIN_STORES>();
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      compiler_fence();
+      __builtin_amdgcn_s_barrier();
+      compiler_fence();
+      issue_stage(d, rot ^ 1, BK);  // slice 1, into the buffer of the previous tile's last slice
+    } else {
+      setup_dma(d, pd, m0, n0, smem);
+      issue_stage(d, 0, 0);
+      issue_stage(d, 1, BK);
+      wait_vmcnt<XMIN>();
+      compiler_fence();
+      __builtin_amdgcn_s_barrier();
+      compiler_fence();
+    }
+    i16x8_t af[2][FM], bf[2][FN];
+    load_frags(af[0], bf[0], smem + rot * STAGE_BYTES, smem + rot * STAGE_BYTES + A_BYTES, 0, wave_m, wave_n,
+               false);
+
+    const int kt_count = (pd.k + BK - 1) / BK;
+    const bool chain = has_next && kt_count >= 2;
+    Dma dn;
+    if (chain) setup_dma(dn, next, ntm * BM, ntn * BN, smem);
+    for (int kt = 0; kt < kt_count; ++kt) {
+      const int b = (kt + rot) & 1;
+      const char* cur = smem + b * STAGE_BYTES;
+      const char* nxt = smem + (b ^ 1) * STAGE_BYTES;
+#pragma unroll
+      for (int kk = 0; kk < KK - 1; ++kk) {
+        load_frags(af[(kk + 1) & 1], bf[(kk + 1) & 1], cur, cur + A_BYTES, kk + 1, wave_m, wave_n, false);
+        mfma_rows<0, FM>(acc, af[kk & 1], bf[kk & 1]);
+        interleave<FM * FN, NDS, 0>();
+      }
+      constexpr int L = (KK - 1) & 1;
+      if (kt + 1 < kt_count) {
+        // As run_tile: slice kt+1 becomes readable, and the drained buffer of slice kt is refilled
+        // with slice kt+2, or with the next tile's slice 0 when slice kt+2 would lie past K.
+        mfma_rows<0, HALF>(acc, af[L], bf[L]);
+        wait_vmcnt<0>();
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        compiler_fence();
+        __builtin_amdgcn_s_barrier();
+        compiler_fence();
+        if (chain && kt + 2 == kt_count)
+          issue_stage(dn, b, 0);
+        else
+          issue_stage(d, b, (kt + 2) * BK);
+        load_frags(af[0], bf[0], nxt, nxt + A_BYTES, 0, wave_m, wave_n, false);
+        mfma_rows<HALF, FM>(acc, af[L], bf[L]);
+        interleave<(FM - HALF) * FN, NDS, NVM>();
+      } else {
+        mfma_rows<0, FM>(acc, af[L], bf[L]);  // the last slice: nothing left to fetch for this tile
+      }
+    }
+    if (chain) {
+      store_tile_counted(acc, pd, m0, n0, wave_m, wave_n);
+      ch.d = dn;
+      ch.rot = (kt_count + rot) & 1;
+      ch.prefetched = true;
+    } else {
+      // Copies of this tile (zero slices past K) landed and every wave is done with LDS before
+      // the next tile's own prologue refills it.
+      wait_vmcnt<0>();
+      compiler_fence();
+      __builtin_amdgcn_s_barrier();
+      compiler_fence();
+      store_tile(acc, pd, m0, n0, wave_m, wave_n, smem);
+      ch.prefetched = false;
+    }
+  }
 };
 
 }  // namespace moegemm

@@ -181,6 +181,23 @@ __device__ __forceinline__ void store4<EF32>(char* dst, f32x4_t v) {
   *MOEGEMM_GLOBAL(f32x4_t, dst) = v;
 }
 
+// Four fp32 values converted to the 16-bit type, as the 8 bytes of one packed pair of dwords.
+template <class E>
+__device__ __forceinline__ u32x2_t pack4(f32x4_t v) {
+  static_assert(E::dtype != DT_F32, "16-bit outputs only");
+  if constexpr (E::dtype == DT_BF16) {
+    typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+    bf16x4_t o;
+    o[0] = (__bf16)v[0]; o[1] = (__bf16)v[1]; o[2] = (__bf16)v[2]; o[3] = (__bf16)v[3];
+    return __builtin_bit_cast(u32x2_t, o);
+  } else {
+    typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+    f16x4_t o;
+    o[0] = (_Float16)v[0]; o[1] = (_Float16)v[1]; o[2] = (_Float16)v[2]; o[3] = (_Float16)v[3];
+    return __builtin_bit_cast(u32x2_t, o);
+  }
+}
+
 // Four fp32 values converted to the 16-bit type, written to LDS (8 bytes).
 template <class E>
 __device__ __forceinline__ void store4_lds(char* dst, f32x4_t v) {
@@ -258,6 +275,7 @@ struct GemmTile {
   static constexpr int PREFIX_OFFSET = 2 * STAGE_BYTES;
   static constexpr int LDS_BYTES = PREFIX_OFFSET + (PREFIX + 1) * 4 + NT * 4;
   static constexpr int WAVES_PER_EU = 1;
+  static constexpr bool CHAIN_OK = false;  // no cross-tile copy chaining (FastTile only)
 
   static_assert(BM % WM == 0 && BN % WN == 0, "tile must split evenly over waves");
   static_assert(WTM % MI == 0 && WTN % MI == 0, "wave tile must be a multiple of the MFMA tile");
@@ -735,6 +753,42 @@ grouped_gemm_kernel(KParams p) {
     tq.drained = 0;
     u = tq.lo(tq.cur) + (int)blockIdx.x / tq.nx;
     if (u >= tq.lo(tq.cur + 1)) next_unit(-1);  // this XCD has fewer units than workgroups
+  }
+  // Two-stage tiles with direct C stores on the static schedule of single and homogeneous launches
+  // chain their copies across tiles (FastTile::run_tile_chained): each tile issues the next unit's
+  // first K slice.
+  if constexpr (T::CHAIN_OK) {
+    if (!stealing && splits == 1 && !p.swiglu && (p.mode == MODE_SINGLE || p.mode == MODE_HOMOGENEOUS)) {
+      auto describe = [&](int unit, ProblemDesc& pd, int& tm, int& tn) {
+        simple_tile<T>(p, unit, pd, tm, tn);
+        pd.swiglu = 0;
+        pd.splits = 1;
+        pd.split = 0;
+        pd.tile = unit;
+        pd.partials = p.partials;
+        pd.counters = p.counters;
+        make_uniform(pd);
+        tm = uniform(tm);
+        tn = uniform(tn);
+      };
+      typename T::Chain ch;
+      ch.rot = 0;
+      ch.prefetched = false;
+      ProblemDesc pd, pdn;
+      int tm = 0, tn = 0, tmn = 0, tnn = 0;
+      if (u < u_end) describe(u, pd, tm, tn);
+      while (u < u_end) {
+        const int un = u + u_step;
+        const bool has_next = un < u_end;
+        if (has_next) describe(un, pdn, tmn, tnn);
+        T::run_tile_chained(pd, tm, tn, smem, pdn, has_next, tmn, tnn, ch);
+        pd = pdn;
+        tm = tmn;
+        tn = tnn;
+        u = un;
+      }
+      return;
+    }
   }
   while (stealing ? u >= 0 : u < u_end) {
     const int t = u % p.total_tiles;
