@@ -57,6 +57,8 @@ constexpr uint32_t kBufferFlags = 0x00020000u;
 constexpr uint32_t kOutOfRange = 0x80000000u;
 // Cache-policy operand of the buffer load/store builtins: sc1, device (agent) scope coherence.
 constexpr int kDeviceCoherent = 16;
+// ... and the non-temporal (streaming) hint.
+constexpr int kNonTemporal = 2;
 
 __device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
 
@@ -656,25 +658,31 @@ struct FastTile {
     store_tile(acc, pd, m0, n0, wave_m, wave_n, smem);
   }
 
-  // Cross-tile chaining, for the two-stage tiles whose C leaves by direct stores (the 16-row decode
-  // tiles).  A workgroup on the static schedule knows its next unit.  So the copy that would fill
-  // the drained buffer with a zero slice past K fetches the next tile's slice 0 instead, and the
-  // next tile starts with that slice in flight.  It sits in the buffer after this tile's last one:
-  // buffer roles rotate by the K slice count at every tile.  This tile's C then leaves by buffer
-  // stores issued with every lane active, exactly CHAIN_STORES per wave; out-of-range lanes are
-  // dropped by the range check.  A wave's vector memory operations complete in issue order, so the
-  // next tile knows its slice 0 has landed once at most CHAIN_STORES operations are outstanding.
-  // It does not wait for the stores themselves.
-  static constexpr bool CHAIN_OK = STAGES == 2 && !STAGED_OK;
-  static constexpr int CHAIN_STORES = FM * FN * (ACC / 4);
+  // Cross-tile chaining of the two-stage tiles.  A workgroup on the static schedule knows its next
+  // unit.  So the copy that would fill the drained buffer with a zero slice past K fetches the next
+  // tile's slice 0 instead, and the next tile starts with that slice in flight.  It sits in the
+  // buffer after this tile's last one: buffer roles rotate by the K slice count at every tile.  This
+  // tile's C then leaves with exactly CHAIN_STORES buffer stores per wave, every lane active;
+  // out-of-range lanes are dropped by the range check.  A wave's vector memory operations complete
+  // in issue order, so the next tile knows its slice 0 has landed once at most CHAIN_STORES
+  // operations are outstanding.  It does not wait for the stores themselves.  Staged tiles stage C
+  // through the wave's slots in the last slice's buffer (the other one holds the prefetch), in
+  // rounds of CH_ROWS rows.  Tiles with more than 64 accumulator registers per wave are left out:
+  // the next tile's copy state and the staging rounds made them spill (194-891 VGPRs on 256x256).
+  static constexpr bool CHAIN_OK = STAGES == 2 && FM * FN * ACC <= 64;
+  static constexpr int CH_ROWS_FIT = STAGED_OK ? (XMIN * 1024 / ROWB) / MI * MI : MI;
+  static constexpr int CH_ROWS = CH_ROWS_FIT < WTM ? CH_ROWS_FIT : WTM;  // staged rows per round
+  static constexpr int CHAIN_STORES = STAGED_OK ? WTM * ROWB / 1024 : FM * FN * (ACC / 4);
   static_assert(!CHAIN_OK || CHAIN_STORES + QA + QB < 64, "outstanding operations must fit the 6-bit vmcnt");
+  static_assert(!(CHAIN_OK && STAGED_OK) || (CH_ROWS > 0 && WTM % CH_ROWS == 0 && (CH_ROWS * ROWB) % 1024 == 0),
+                "staging rounds must cover the wave tile in whole slots");
   struct Chain {
     Dma d;            // copy state of the tile whose slice 0 the previous tile issued
     int rot;          // LDS buffer holding that slice 0
     bool prefetched;  // false: the next tile issues its own prologue
   };
 
-  // C stores with a fixed instruction count per wave: CHAIN_STORES 8-byte buffer stores.
+  // Direct C stores with a fixed instruction count per wave: CHAIN_STORES 8-byte buffer stores.
   __device__ static __forceinline__ void store_tile_counted(const acc_t (&acc)[FM][FN], const ProblemDesc& pd,
                                                             int m0, int n0, int wave_m, int wave_n) {
     const int lane = threadIdx.x & 63;
@@ -699,12 +707,62 @@ struct FastTile {
     }
   }
 
+  // Staged C stores with a fixed instruction count per wave: the wave's sub-tile in rounds of
+  // CH_ROWS rows through its XMIN slots of LDS buffer `stage` (layout as in staged_store), each
+  // round's rows leaving as 16-byte buffer stores along the rows: CHAIN_STORES in all.  Needs a
+  // 16-byte aligned C with a row pitch of a multiple of 8 elements.
+  __device__ static __forceinline__ void staged_store_counted(const acc_t (&acc)[FM][FN], const ProblemDesc& pd,
+                                                              int m0, int n0, int wave_m, int wave_n, char* smem,
+                                                              int stage) {
+    static_assert(STAGED_OK, "tile cannot stage its C sub-tile");
+    constexpr int FMR = CH_ROWS / MI;  // fragment rows per round
+    constexpr int RPI = 1024 / ROWB;   // rows per 1 KiB read
+    // Full 128-byte lines stream through L2 as non-temporal stores (as in staged_store).
+    constexpr int kAux = ROWB >= 128 ? kNonTemporal : 0;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int rows = min(BM, pd.m - m0);
+    const auto rc = __builtin_amdgcn_make_buffer_rsrc(pd.c + (int64_t)m0 * pd.scm * 2, (short)0,
+                                                      (int)((uint32_t)rows * (uint32_t)pd.scm * 2u), (int)kBufferFlags);
+#pragma unroll
+    for (int rd = 0; rd < WTM / CH_ROWS; ++rd) {
+#pragma unroll
+      for (int f = 0; f < FMR; ++f) {
+        const int fm = rd * FMR + f;
+        const int r = f * MI + (lane % MI);
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+          for (int q = 0; q < ACC / 4; ++q) {
+            const int c = fn * MI + ((MI == 32) ? (q * 8 + (lane >> 5) * 4) : ((lane >> 4) * 4));
+            const int lin = r * ROWB + (((c >> 3) ^ (r % ROW_CHUNKS)) << 4) + (c & 7) * 2;
+            const f32x4_t v = {acc[fm][fn][q * 4 + 0], acc[fm][fn][q * 4 + 1], acc[fm][fn][q * 4 + 2],
+                               acc[fm][fn][q * 4 + 3]};
+            store4_lds<E>(smem + owned_slot(stage * XMIN + (lin >> 10), wave) + (lin & 1023), v);
+          }
+      }
+      compiler_fence();
+#pragma unroll
+      for (int j = 0; j < CH_ROWS * ROWB / 1024; ++j) {
+        const int r = j * RPI + lane / ROW_CHUNKS, chunk = lane % ROW_CHUNKS;
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(smem + owned_slot(stage * XMIN + j, wave) +
+                                                            (r % RPI) * ROWB + ((chunk ^ (r % ROW_CHUNKS)) << 4));
+        const int rl = wave_m * WTM + rd * CH_ROWS + r;
+        const int gn = n0 + wave_n * WTN + chunk * 8;
+        const uint32_t off =
+            (rl < rows && gn < pd.n) ? ((uint32_t)rl * (uint32_t)pd.scm + (uint32_t)gn) * 2u : kOutOfRange;
+        __builtin_amdgcn_raw_buffer_store_b128(v, rc, (int)off, 0, kAux);
+      }
+      compiler_fence();
+    }
+  }
+
   // run_tile's schedule for CHAIN_OK tiles; `next` is the workgroup's next tile when `has_next`.
   // `ch` carries the prefetch from one call to the next; start a workgroup with ch.prefetched false.
   __device__ static __forceinline__ void run_tile_chained(const ProblemDesc& pd, int tm, int tn, char* smem,
                                                           const ProblemDesc& next, bool has_next, int ntm, int ntn,
                                                           Chain& ch) {
-    static_assert(CHAIN_OK, "the chained schedule is for two-stage tiles with direct C stores");
+    static_assert(CHAIN_OK, "the chained schedule is for two-stage tiles");
     static_assert(KK % 2 == 0, "fragment double buffer alternates by K step");
     constexpr int HALF = FM / 2 > 0 ? FM / 2 : 1;
     constexpr int NDS = FM + 2 * FN;
@@ -748,9 +806,8 @@ struct FastTile {
                false);
 
     const int kt_count = (pd.k + BK - 1) / BK;
-    const bool chain = has_next && kt_count >= 2;
-    Dma dn;
-    if (chain) setup_dma(dn, next, ntm * BM, ntn * BN, smem);
+    const bool c16 = ((reinterpret_cast<uintptr_t>(pd.c) & 15) == 0) && (pd.scm & 7) == 0;
+    const bool chain = has_next && kt_count >= 2 && (!STAGED_OK || c16);
     for (int kt = 0; kt < kt_count; ++kt) {
       const int b = (kt + rot) & 1;
       const char* cur = smem + b * STAGE_BYTES;
@@ -771,10 +828,13 @@ struct FastTile {
         compiler_fence();
         __builtin_amdgcn_s_barrier();
         compiler_fence();
-        if (chain && kt + 2 == kt_count)
-          issue_stage(dn, b, 0);
-        else
+        if (chain && kt + 2 == kt_count) {
+          // The next tile's copy state goes straight into `ch` (this tile's `d` is no longer needed).
+          setup_dma(ch.d, next, ntm * BM, ntn * BN, smem);
+          issue_stage(ch.d, b, 0);
+        } else {
           issue_stage(d, b, (kt + 2) * BK);
+        }
         load_frags(af[0], bf[0], nxt, nxt + A_BYTES, 0, wave_m, wave_n, false);
         mfma_rows<HALF, FM>(acc, af[L], bf[L]);
         interleave<(FM - HALF) * FN, NDS, NVM>();
@@ -783,18 +843,48 @@ struct FastTile {
       }
     }
     if (chain) {
-      store_tile_counted(acc, pd, m0, n0, wave_m, wave_n);
-      ch.d = dn;
+      if constexpr (STAGED_OK) {
+        // Every wave has read the last slice's buffer before any stages C in its slots there.
+        const int last = (kt_count - 1 + rot) & 1;
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        compiler_fence();
+        __builtin_amdgcn_s_barrier();
+        compiler_fence();
+        staged_store_counted(acc, pd, m0, n0, wave_m, wave_n, smem, last);
+      } else {
+        store_tile_counted(acc, pd, m0, n0, wave_m, wave_n);
+      }
       ch.rot = (kt_count + rot) & 1;
       ch.prefetched = true;
     } else {
       // Copies of this tile (zero slices past K) landed and every wave is done with LDS before
-      // the next tile's own prologue refills it.
+      // the next tile's own prologue refills it.  Chained launches have no split-K and no SwiGLU,
+      // so only the plain C epilogue is needed.
       wait_vmcnt<0>();
       compiler_fence();
       __builtin_amdgcn_s_barrier();
       compiler_fence();
-      store_tile(acc, pd, m0, n0, wave_m, wave_n, smem);
+      if constexpr (STAGED_OK) {
+        staged_store(acc, pd, m0, n0, wave_m, wave_n, smem);
+      } else {
+        const int lane = threadIdx.x & 63;
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm) {
+          const int gm = m0 + wave_m * WTM + fm * MI + (lane % MI);
+          if (gm >= pd.m) continue;
+          char* crow = pd.c + (int64_t)gm * pd.scm * 2;
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+            for (int q = 0; q < ACC / 4; ++q) {
+              const int nloc = (MI == 32) ? (q * 8 + (lane >> 5) * 4) : ((lane >> 4) * 4);
+              const int gn = n0 + wave_n * WTN + fn * MI + nloc;
+              if (gn < pd.n)
+                store4<E>(crow + (int64_t)gn * 2, f32x4_t{acc[fm][fn][q * 4 + 0], acc[fm][fn][q * 4 + 1],
+                                                          acc[fm][fn][q * 4 + 2], acc[fm][fn][q * 4 + 3]});
+            }
+        }
+      }
       ch.prefetched = false;
     }
   }
