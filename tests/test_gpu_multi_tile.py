@@ -104,3 +104,46 @@ def test_single_every_tile_column_slice_small_grids(dtype, pitch_pad):
             assert torch.equal(c, expected), label
             assert torch.isnan(wide[0]).all() and torch.isnan(wide[m + 1]).all(), label
             assert torch.isnan(wide[:, n:]).all(), label
+
+
+@pytest.mark.parametrize("k", [64, 128, 136, 192, 256, 328])
+def test_chained_two_stage_tiles_every_k_slice_count(k):
+    """Two-stage tiles chain each tile's copies into the next tile's first K slice on the static
+    schedule (single and homogeneous launches).  K from one slice (no chaining) to several with a
+    tail, ragged M and N, several tiles per workgroup and C alternating 16- and 8-byte alignment
+    (staged tiles chain only for 16-byte aligned C): exact integers and intact guard bands."""
+    from kernels import _native
+    from kernels.grouped_gemm import build_grouped_workspace
+
+    dtype = torch.bfloat16
+    groups, m, n = 6, 70, 392
+    ws = build_grouped_workspace([(m, k, n)] * groups, dtype, seed=2)
+    storages = []
+    for e in range(groups):
+        ws.a[e].copy_(_ints((m, k), dtype))
+        ws.b[e].copy_(_ints((k, n), dtype))
+        lead = GUARD + (4 if e % 3 == 1 else 0)
+        storage = torch.full((lead + m * n + GUARD,), float("nan"), device="cuda", dtype=dtype)
+        ws.c[e] = storage[lead:lead + m * n].view(m, n)
+        ws.c_ptrs[e] = ws.c[e].data_ptr()
+        storages.append((storage, lead))
+    code = _native.dtype_code(dtype)
+    expected = [(a.double() @ b.double()).to(dtype) for a, b, _ in ws.problem_tensors()]
+    two_stage = [t for t in _tiles(dtype) if t[4] == 2 and t[0] <= 64]
+    assert two_stage
+    for bm, bn, bk, warps, stages in two_stage:
+        tiles = groups * -(-m // bm) * -(-n // bn)
+        for grid in sorted({1, 5, 8, max(1, tiles // 4)}):
+            print(f"chained k={k} tile={(bm, bn, bk, warps, stages)} tiles={tiles} grid={grid}", flush=True)
+            for storage, _ in storages:
+                storage.fill_(float("nan"))
+            status = _native.library().moegemm_grouped_gemm(
+                ws.a_ptrs.data_ptr(), ws.b_ptrs.data_ptr(), ws.c_ptrs.data_ptr(), ws.dims.data_ptr(),
+                ws.strides.data_ptr(), groups, m, n, k, 1, tiles, code, 0, bm, bn, bk, 4, warps, stages, grid, 1,
+                _native.current_stream_handle(ws.a[0].device))
+            _native.check(status)
+            torch.cuda.synchronize()
+            for e, ((storage, lead), ref) in enumerate(zip(storages, expected)):
+                label = f"k {k} tile {(bm, bn, bk, warps, stages)} grid {grid} problem {e}"
+                assert torch.equal(ws.c[e], ref), label
+                assert torch.isnan(storage[:lead]).all() and torch.isnan(storage[lead + m * n:]).all(), label
