@@ -668,7 +668,8 @@ struct FastTile {
   // operations are outstanding.  It does not wait for the stores themselves.  Staged tiles stage C
   // through the wave's slots in the last slice's buffer (the other one holds the prefetch), in
   // rounds of CH_ROWS rows.  Tiles with more than 64 accumulator registers per wave are left out:
-  // the next tile's copy state and the staging rounds made them spill (194-891 VGPRs on 256x256).
+  // the next tile's copy state and the staging rounds made them spill (the 8-wave 256x256x64 tile
+  // from 7 to about 200 spilled VGPRs).
   static constexpr bool CHAIN_OK = STAGES == 2 && FM * FN * ACC <= 64;
   static constexpr int CH_ROWS_FIT = STAGED_OK ? (XMIN * 1024 / ROWB) / MI * MI : MI;
   static constexpr int CH_ROWS = CH_ROWS_FIT < WTM ? CH_ROWS_FIT : WTM;  // staged rows per round
