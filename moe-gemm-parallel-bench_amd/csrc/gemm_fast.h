@@ -678,8 +678,7 @@ struct FastTile {
   static_assert(!(CHAIN_OK && STAGED_OK) || (CH_ROWS > 0 && WTM % CH_ROWS == 0 && (CH_ROWS * ROWB) % 1024 == 0),
                 "staging rounds must cover the wave tile in whole slots");
   struct Chain {
-    Dma d;            // copy state of the tile whose slice 0 the previous tile issued
-    int rot;          // LDS buffer holding that slice 0
+    int rot;          // LDS buffer holding the slice 0 the previous tile issued
     bool prefetched;  // false: the next tile issues its own prologue
   };
 
@@ -785,7 +784,9 @@ struct FastTile {
     if (ch.prefetched) {
       // Slice 0 was issued before the previous tile's CHAIN_STORES stores, with nothing else of
       // this wave outstanding; the previous tile's LDS reads are done once every wave is here.
-      d = ch.d;
+      // The copy state is recomputed rather than carried (fewer registers live across the
+      // previous tile's epilogue).
+      setup_dma(d, pd, m0, n0, smem);
       rot = ch.rot;
       wait_vmcnt<CHAIN_STORES>();
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -830,9 +831,9 @@ struct FastTile {
         __builtin_amdgcn_s_barrier();
         compiler_fence();
         if (chain && kt + 2 == kt_count) {
-          // The next tile's copy state goes straight into `ch` (this tile's `d` is no longer needed).
-          setup_dma(ch.d, next, ntm * BM, ntn * BN, smem);
-          issue_stage(ch.d, b, 0);
+          Dma dn;  // the next tile's copy state, only for its slice 0
+          setup_dma(dn, next, ntm * BM, ntn * BN, smem);
+          issue_stage(dn, b, 0);
         } else {
           issue_stage(d, b, (kt + 2) * BK);
         }
