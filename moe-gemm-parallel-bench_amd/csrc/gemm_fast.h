@@ -667,10 +667,12 @@ struct FastTile {
   // in issue order, so the next tile knows its slice 0 has landed once at most CHAIN_STORES
   // operations are outstanding.  It does not wait for the stores themselves.  Staged tiles stage C
   // through the wave's slots in the last slice's buffer (the other one holds the prefetch), in
-  // rounds of CH_ROWS rows.  Tiles with more than 64 accumulator registers per wave are left out:
-  // the next tile's copy state and the staging rounds made them spill (the 8-wave 256x256x64 tile
-  // from 7 to about 200 spilled VGPRs).
-  static constexpr bool CHAIN_OK = STAGES == 2 && FM * FN * ACC <= 64;
+  // rounds of CH_ROWS rows.  Workgroup tiles over 32768 outputs are left out: the chained loop
+  // made them spill (the 8-wave 256x256x64 tile from 7 to about 200 spilled VGPRs).  Tiles with
+  // more than 64 accumulator registers per wave chain only short-K launches (CHAIN_MAX_SLICES):
+  // 64x512x64 gained 8 % at K = 256 (4 slices) and lost 2-3 % at K = 2048 (32 slices).
+  static constexpr bool CHAIN_OK = STAGES == 2 && FM * FN * ACC <= 128 && BM * BN <= 32768;
+  static constexpr int CHAIN_MAX_SLICES = FM * FN * ACC <= 64 ? (1 << 30) : 8;
   static constexpr int CH_ROWS_FIT = STAGED_OK ? (XMIN * 1024 / ROWB) / MI * MI : MI;
   static constexpr int CH_ROWS = CH_ROWS_FIT < WTM ? CH_ROWS_FIT : WTM;  // staged rows per round
   static constexpr int CHAIN_STORES = STAGED_OK ? WTM * ROWB / 1024 : FM * FN * (ACC / 4);

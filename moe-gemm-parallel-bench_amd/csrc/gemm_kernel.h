@@ -754,11 +754,11 @@ grouped_gemm_kernel(KParams p) {
     u = tq.lo(tq.cur) + (int)blockIdx.x / tq.nx;
     if (u >= tq.lo(tq.cur + 1)) next_unit(-1);  // this XCD has fewer units than workgroups
   }
-  // Two-stage tiles with direct C stores on the static schedule of single and homogeneous launches
-  // chain their copies across tiles (FastTile::run_tile_chained): each tile issues the next unit's
-  // first K slice.
+  // Two-stage tiles on the static schedule of single and homogeneous launches chain their copies
+  // across tiles (FastTile::run_tile_chained): each tile issues the next unit's first K slice.
   if constexpr (T::CHAIN_OK) {
-    if (!stealing && splits == 1 && !p.swiglu && (p.mode == MODE_SINGLE || p.mode == MODE_HOMOGENEOUS)) {
+    if (!stealing && splits == 1 && !p.swiglu && (p.mode == MODE_SINGLE || p.mode == MODE_HOMOGENEOUS) &&
+        (p.K + T::BK - 1) / T::BK <= T::CHAIN_MAX_SLICES) {
       auto describe = [&](int unit, ProblemDesc& pd, int& tm, int& tn) {
         simple_tile<T>(p, unit, pd, tm, tn);
         pd.swiglu = 0;
