@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define MOEGEMM_ABI_VERSION 6
+#define MOEGEMM_ABI_VERSION 7
 
 #define MOEGEMM_OK 0
 #define MOEGEMM_ERR_INVALID (-1)   /* bad shape, pointer, dtype or parameter (Python: ValueError) */
@@ -36,8 +36,9 @@ extern "C" {
 #define MOEGEMM_PRECISION_IEEE 0 /* operands used as given */
 #define MOEGEMM_PRECISION_TF32 1 /* fp32 operands rounded to a 10-bit mantissa (ties away) */
 
-/* Size of the tile queue of the work-stealing launches (int32 counters, 256-byte aligned). */
-#define MOEGEMM_QUEUE_BYTES 256
+/* Size of the tile queue of the work-stealing launches (17 int32 counters, each in a 256-byte
+ * block of its own; the buffer is 256-byte aligned). */
+#define MOEGEMM_QUEUE_BYTES 4352
 
 /* ABI version of the loaded library (MOEGEMM_ABI_VERSION when header and library agree). */
 int moegemm_abi_version(void);

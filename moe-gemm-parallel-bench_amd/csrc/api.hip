@@ -212,7 +212,7 @@ namespace {
 int set_queue(KParams& p, void* queue) {
   if (queue && (reinterpret_cast<uintptr_t>(queue) & 255))
     return fail(MOEGEMM_ERR_INVALID, "the tile queue must be 256-byte aligned");
-  static_assert((kQueues + 1) * 4 <= MOEGEMM_QUEUE_BYTES, "queue counters fit the documented size");
+  static_assert(kQueueSlots * kQueueStride * 4 <= MOEGEMM_QUEUE_BYTES, "queue counters fit the documented size");
   p.queue = static_cast<int32_t*>(queue);
   return MOEGEMM_OK;
 }

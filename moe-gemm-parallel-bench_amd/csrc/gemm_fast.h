@@ -759,11 +759,23 @@ struct FastTile {
     }
   }
 
-  // run_tile's schedule for CHAIN_OK tiles; `next` is the workgroup's next tile when `has_next`.
-  // `ch` carries the prefetch from one call to the next; start a workgroup with ch.prefetched false.
-  __device__ static __forceinline__ void run_tile_chained(const ProblemDesc& pd, int tm, int tn, char* smem,
-                                                          const ProblemDesc& next, bool has_next, int ntm, int ntn,
-                                                          Chain& ch) {
+  // run_tile's schedule for CHAIN_OK tiles.  `ch` carries the prefetch from one call to the next;
+  // start a workgroup with ch.prefetched false.  The workgroup's next tile comes from `sched`, whose
+  // hooks every wave runs once per tile, in this order:
+  //   sched.started()               after the tile's slice-1 copies are issued.  The wave's next
+  //                                 vector-memory wait is vmcnt(0), so one more vector memory
+  //                                 operation issued here never breaks a counted wait;
+  //   sched.before_barrier()        after that vmcnt(0) wait, before the barrier of the first slice
+  //                                 boundary (of the epilogue for a one-slice tile); LDS writes
+  //                                 made here are visible after the barrier;
+  //   sched.next(next, ntm, ntn)    after that barrier: true and the next tile's description, or
+  //                                 false when this is the workgroup's last tile.  The next tile is
+  //                                 needed no earlier: its slice 0 is issued at the boundary before
+  //                                 this tile's last slice.
+  // Returns whether there is a next tile (then `next`, `ntm`, `ntn` describe it).
+  template <class Sched>
+  __device__ static __forceinline__ bool run_tile_chained(const ProblemDesc& pd, int tm, int tn, char* smem, Chain& ch,
+                                                          Sched& sched, ProblemDesc& next, int& ntm, int& ntn) {
     static_assert(CHAIN_OK, "the chained schedule is for two-stage tiles");
     static_assert(KK % 2 == 0, "fragment double buffer alternates by K step");
     constexpr int HALF = FM / 2 > 0 ? FM / 2 : 1;
@@ -805,13 +817,15 @@ struct FastTile {
       __builtin_amdgcn_s_barrier();
       compiler_fence();
     }
+    sched.started();
+    bool has_next = false;
     i16x8_t af[2][FM], bf[2][FN];
     load_frags(af[0], bf[0], smem + rot * STAGE_BYTES, smem + rot * STAGE_BYTES + A_BYTES, 0, wave_m, wave_n,
                false);
 
     const int kt_count = (pd.k + BK - 1) / BK;
     const bool c16 = ((reinterpret_cast<uintptr_t>(pd.c) & 15) == 0) && (pd.scm & 7) == 0;
-    const bool chain = has_next && kt_count >= 2 && (!STAGED_OK || c16);
+    bool chain = false;  // set at the first slice boundary, once the next tile is known
     for (int kt = 0; kt < kt_count; ++kt) {
       const int b = (kt + rot) & 1;
       const char* cur = smem + b * STAGE_BYTES;
@@ -828,10 +842,15 @@ struct FastTile {
         // with slice kt+2, or with the next tile's slice 0 when slice kt+2 would lie past K.
         mfma_rows<0, HALF>(acc, af[L], bf[L]);
         wait_vmcnt<0>();
+        if (kt == 0) sched.before_barrier();
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         compiler_fence();
         __builtin_amdgcn_s_barrier();
         compiler_fence();
+        if (kt == 0) {
+          has_next = sched.next(next, ntm, ntn);
+          chain = has_next && (!STAGED_OK || c16);
+        }
         if (chain && kt + 2 == kt_count) {
           Dma dn;  // the next tile's copy state, only for its slice 0
           setup_dma(dn, next, ntm * BM, ntn * BN, smem);
@@ -865,9 +884,12 @@ struct FastTile {
       // the next tile's own prologue refills it.  Chained launches have no split-K and no SwiGLU,
       // so only the plain C epilogue is needed.
       wait_vmcnt<0>();
+      if (kt_count <= 1) sched.before_barrier();
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       compiler_fence();
       __builtin_amdgcn_s_barrier();
       compiler_fence();
+      if (kt_count <= 1) has_next = sched.next(next, ntm, ntn);
       if constexpr (STAGED_OK) {
         staged_store(acc, pd, m0, n0, wave_m, wave_n, smem);
       } else {
@@ -891,6 +913,7 @@ struct FastTile {
       }
       ch.prefetched = false;
     }
+    return has_next;
   }
 };
 

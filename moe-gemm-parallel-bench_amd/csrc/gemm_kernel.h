@@ -78,8 +78,9 @@ struct KParams {
   int32_t k_chunk;
   float* partials;
   int32_t* counters;
-  // Work-stealing schedule (null = static): kQueues ticket counters, then one exit count; zero
-  // between launches (the last workgroup of a launch re-arms them).
+  // Work-stealing schedule (null = static): ticket counters and exit counts, one per 256-byte
+  // block (the layout is at kQueueStride); zero between launches (the last workgroup of a launch
+  // re-arms them).
   int32_t* queue;
 };
 
@@ -621,8 +622,16 @@ __device__ __forceinline__ void load_prefix(const KParams& p, int* s_pref, int* 
 // counters at once (one lane each) and moves to the queue with the most units left, so units left
 // on a slow XCD are taken by idle ones and a drained workgroup learns that every queue is empty in
 // one round trip.  Every workgroup counts itself out in queue[kQueues] after its last claim has
-// returned, and the last one re-arms all counters to zero for the next launch.
+// returned, and the last one re-arms all counters to zero for the next launch.  Chained two-stage
+// tiles draw one unit further ahead (see the chained loop of grouped_gemm_kernel).
 constexpr int kQueues = 8;
+// Counters of the queue buffer, each in a 256-byte block of its own (int32 index = slot *
+// kQueueStride): tickets of queue y in slot y, the exit count of the workgroups b with b % 8 == x
+// in slot kQueues + x, and the exit count of those eight groups in slot 2 * kQueues.  Device-scope
+// atomics are performed at the memory side; counters that shared one cache line serialised every
+// claim and exit of a launch there.
+constexpr int kQueueStride = 64;
+constexpr int kQueueSlots = 2 * kQueues + 1;
 
 struct TileQueue {
   int32_t* q;
@@ -630,7 +639,9 @@ struct TileQueue {
   int cur;           // queue of the last claim (starts at this workgroup's XCD)
   uint32_t drained;  // bit y: queue y has no units left (known to wave 0)
 
-  __device__ int lo(int y) const { return (int)((int64_t)y * units / nx); }
+  int lg;            // log2(nx): nx is 8 or 1
+
+  __device__ int lo(int y) const { return (int)(((int64_t)y * units) >> lg); }
 
   // Wave 0 only (every lane, uniform control flow).  Lane 0 holds `c`, a ticket already drawn from
   // queue `cur`, or -1.  Returns the next unit, or -1 when every queue is drained.  Each round
@@ -641,7 +652,7 @@ struct TileQueue {
       if (!((drained >> cur) & 1u)) {
         int u = -1;
         if (lane == 0) {
-          if (c < 0) c = atomicAdd(q + cur, 1);
+          if (c < 0) c = atomicAdd(q + cur * kQueueStride, 1);
           u = lo(cur) + per + c;
           if (u >= lo(cur + 1)) u = -1;
         }
@@ -652,7 +663,8 @@ struct TileQueue {
       }
       int left = 0;
       if (lane < nx && !((drained >> lane) & 1u))
-        left = lo(lane + 1) - lo(lane) - per - __hip_atomic_load(q + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        left = lo(lane + 1) - lo(lane) - per -
+               __hip_atomic_load(q + lane * kQueueStride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       drained |= (uint32_t)__builtin_amdgcn_ballot_w64(lane < nx && left <= 0) & ((1u << nx) - 1u);
       int best = -1, most = 0;
       for (int y = 0; y < nx; ++y) {
@@ -668,6 +680,18 @@ struct TileQueue {
     return -1;
   }
 };
+
+// The three schedule hooks of FastTile::run_tile_chained, as one object.
+template <class BeforeBarrier, class Next, class Started>
+struct ChainHooks {
+  BeforeBarrier before_barrier;
+  Next next;
+  Started started;
+};
+template <class BeforeBarrier, class Next, class Started>
+__device__ __forceinline__ ChainHooks<BeforeBarrier, Next, Started> chain_hooks(BeforeBarrier b, Next n, Started s) {
+  return {b, n, s};
+}
 
 // Problem and tile coordinates of tile t in a single or homogeneous launch (unsplit fields only).
 template <class T>
@@ -747,6 +771,7 @@ grouped_gemm_kernel(KParams p) {
   if (stealing) {
     tq.q = p.queue;
     tq.nx = (grid & 7) == 0 ? kQueues : 1;
+    tq.lg = tq.nx == kQueues ? 3 : 0;
     tq.per = grid / tq.nx;
     tq.units = units;
     tq.cur = (int)blockIdx.x & (tq.nx - 1);
@@ -754,10 +779,31 @@ grouped_gemm_kernel(KParams p) {
     u = tq.lo(tq.cur) + (int)blockIdx.x / tq.nx;
     if (u >= tq.lo(tq.cur + 1)) next_unit(-1);  // this XCD has fewer units than workgroups
   }
-  // Two-stage tiles on the static schedule of single and homogeneous launches chain their copies
-  // across tiles (FastTile::run_tile_chained): each tile issues the next unit's first K slice.
+  // Every workgroup counts itself out of the stealing queues after its last claim has returned, in
+  // two levels: into the exit count of its group (b % 8), and the group's last member into the
+  // count of groups.  The last group's last member re-arms every counter for the next launch.
+  auto count_out = [&] {
+    if (stealing && threadIdx.x == 0) {
+      const int x = (int)blockIdx.x & 7;
+      const int members = (grid - x + 7) >> 3, groups = min(grid, 8);
+      if (atomicAdd(p.queue + (kQueues + x) * kQueueStride, 1) == members - 1 &&
+          atomicAdd(p.queue + 2 * kQueues * kQueueStride, 1) == groups - 1) {
+        for (int y = 0; y < kQueueSlots; ++y) atomicExch(p.queue + y * kQueueStride, 0);
+      }
+    }
+  };
+  // Two-stage tiles of single and homogeneous launches chain their copies across tiles
+  // (FastTile::run_tile_chained): each tile issues the next unit's first K slice at the boundary
+  // before its last slice, so the next unit must be known by then.  The static schedule knows it in
+  // advance.  Under work stealing, lane 0 of wave 0 draws the ticket for the next unit once the
+  // tile's slice-1 copies are issued, and wave 0 resolves it at the tile's first slice boundary,
+  // before the barrier that publishes it to the workgroup.  Each tile claims exactly its successor,
+  // as the unchained loop does, only earlier: a workgroup never holds more than one unit ahead, so
+  // the last units of a queue still go to whichever workgroups reach them first.  Every ticket is
+  // resolved within the tile that drew it, so none is outstanding when the workgroup counts itself
+  // out.
   if constexpr (T::CHAIN_OK) {
-    if (!stealing && splits == 1 && !p.swiglu && (p.mode == MODE_SINGLE || p.mode == MODE_HOMOGENEOUS) &&
+    if (splits == 1 && !p.swiglu && (p.mode == MODE_SINGLE || p.mode == MODE_HOMOGENEOUS) &&
         (p.K + T::BK - 1) / T::BK <= T::CHAIN_MAX_SLICES) {
       auto describe = [&](int unit, ProblemDesc& pd, int& tm, int& tn) {
         simple_tile<T>(p, unit, pd, tm, tn);
@@ -771,22 +817,45 @@ grouped_gemm_kernel(KParams p) {
         tm = uniform(tm);
         tn = uniform(tn);
       };
+      int ticket = -1;  // lane 0 of wave 0: drawn from queue tq.cur, not yet resolved
+      auto hooks = chain_hooks(
+          [&] {
+            if (stealing && threadIdx.x < 64) {
+              const int claimed = tq.claim(ticket);
+              if (threadIdx.x == 0) s_next[parity] = claimed;
+              ticket = -1;
+            }
+          },
+          [&](ProblemDesc& next, int& ntm, int& ntn) -> bool {
+            if (stealing) {
+              u = uniform(s_next[parity]);
+              parity ^= 1;
+            } else {
+              u += u_step;
+              if (u >= u_end) u = -1;
+            }
+            if (u < 0) return false;
+            describe(u, next, ntm, ntn);
+            return true;
+          },
+          [&] {
+            if (stealing && threadIdx.x == 0 && !((tq.drained >> tq.cur) & 1u))
+              ticket = atomicAdd(tq.q + tq.cur * kQueueStride, 1);
+          });
       typename T::Chain ch;
       ch.rot = 0;
       ch.prefetched = false;
       ProblemDesc pd, pdn;
       int tm = 0, tn = 0, tmn = 0, tnn = 0;
-      if (u < u_end) describe(u, pd, tm, tn);
-      while (u < u_end) {
-        const int un = u + u_step;
-        const bool has_next = un < u_end;
-        if (has_next) describe(un, pdn, tmn, tnn);
-        T::run_tile_chained(pd, tm, tn, smem, pdn, has_next, tmn, tnn, ch);
-        pd = pdn;
-        tm = tmn;
-        tn = tnn;
-        u = un;
+      if (stealing ? u >= 0 : u < u_end) {
+        describe(u, pd, tm, tn);
+        while (T::run_tile_chained(pd, tm, tn, smem, ch, hooks, pdn, tmn, tnn)) {
+          pd = pdn;
+          tm = tmn;
+          tn = tnn;
+        }
       }
+      count_out();
       return;
     }
   }
@@ -859,17 +928,15 @@ grouped_gemm_kernel(KParams p) {
     make_uniform(pd);
     int ticket = -1;  // the next unit's ticket: drawn before the C stores, resolved after the tile
     T::run_tile(pd, uniform(tm), uniform(tn), smem, p.tf32 != 0, [&] {
-      if (stealing && threadIdx.x == 0 && !((tq.drained >> tq.cur) & 1u)) ticket = atomicAdd(tq.q + tq.cur, 1);
+      if (stealing && threadIdx.x == 0 && !((tq.drained >> tq.cur) & 1u))
+        ticket = atomicAdd(tq.q + tq.cur * kQueueStride, 1);
     });
     if (stealing)
       next_unit(ticket);
     else
       u += u_step;
   }
-  if (stealing && threadIdx.x == 0 && atomicAdd(p.queue + kQueues, 1) == grid - 1) {
-    for (int y = 0; y < kQueues; ++y) atomicExch(p.queue + y, 0);
-    atomicExch(p.queue + kQueues, 0);
-  }
+  count_out();
 }
 
 }  // namespace moegemm

@@ -15,7 +15,7 @@ from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().with_name("libmoegemm.so")
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 OK = 0
 ERR_INVALID = -1
 ERR_NO_KERNEL = -2
@@ -204,7 +204,7 @@ def splitk_workspace(device, stream_handle: int, nbytes: int):
 
 # Work-stealing tile queues, one per (device, stream), zeroed once and never released (launches
 # leave them zero; a captured graph keeps a valid address).
-QUEUE_BYTES = 256
+QUEUE_BYTES = 4352
 NOALLOC_SCRATCH_BYTES = 64 * 1024 * 1024 + 256 * 1024  # MOEGEMM_NOALLOC_SCRATCH_BYTES
 TILE_SCHEDULES = ("static", "stealing")
 _TILE_QUEUES: dict[tuple[int, int], object] = {}

@@ -1,4 +1,4 @@
-"""GPU tests of workgroups that run several tiles in a row on the static schedule.
+"""GPU tests of workgroups that run several tiles in a row (static and work-stealing schedules).
 
 Each tile's epilogue stages C in the LDS slots that the next tile's copies refill, so a tile must
 leave nothing behind for its successor.  Exact-integer results (small integers in A and B, so the
@@ -106,12 +106,14 @@ def test_single_every_tile_column_slice_small_grids(dtype, pitch_pad):
             assert torch.isnan(wide[:, n:]).all(), label
 
 
+@pytest.mark.parametrize("schedule", ["static", "stealing"])
 @pytest.mark.parametrize("k", [64, 128, 136, 192, 256, 328])
-def test_chained_two_stage_tiles_every_k_slice_count(k):
-    """Two-stage tiles chain each tile's copies into the next tile's first K slice on the static
-    schedule (single and homogeneous launches).  K from one slice (no chaining) to several with a
-    tail, ragged M and N, several tiles per workgroup and C alternating 16- and 8-byte alignment
-    (staged tiles chain only for 16-byte aligned C): exact integers and intact guard bands."""
+def test_chained_two_stage_tiles_every_k_slice_count(k, schedule):
+    """Two-stage tiles chain each tile's copies into the next tile's first K slice (single and
+    homogeneous launches).  On the stealing schedule the workgroup claims its units one ahead.  K
+    from one slice (no chaining) to several with a tail, ragged M and N, several tiles per
+    workgroup and C alternating 16- and 8-byte alignment (staged tiles chain only for 16-byte
+    aligned C): exact integers, intact guard bands, and a re-armed queue after every launch."""
     from kernels import _native
     from kernels.grouped_gemm import build_grouped_workspace
 
@@ -134,16 +136,22 @@ def test_chained_two_stage_tiles_every_k_slice_count(k):
     for bm, bn, bk, warps, stages in two_stage:
         tiles = groups * -(-m // bm) * -(-n // bn)
         for grid in sorted({1, 5, 8, max(1, tiles // 4)}):
-            print(f"chained k={k} tile={(bm, bn, bk, warps, stages)} tiles={tiles} grid={grid}", flush=True)
+            print(f"chained {schedule} k={k} tile={(bm, bn, bk, warps, stages)} tiles={tiles} grid={grid}", flush=True)
             for storage, _ in storages:
                 storage.fill_(float("nan"))
-            status = _native.library().moegemm_grouped_gemm(
-                ws.a_ptrs.data_ptr(), ws.b_ptrs.data_ptr(), ws.c_ptrs.data_ptr(), ws.dims.data_ptr(),
-                ws.strides.data_ptr(), groups, m, n, k, 1, tiles, code, 0, bm, bn, bk, 4, warps, stages, grid, 1,
-                _native.current_stream_handle(ws.a[0].device))
+            args = (ws.a_ptrs.data_ptr(), ws.b_ptrs.data_ptr(), ws.c_ptrs.data_ptr(), ws.dims.data_ptr(),
+                    ws.strides.data_ptr(), groups, m, n, k, 1, tiles, code, 0, bm, bn, bk, 4, warps, stages, grid, 1)
+            stream = _native.current_stream_handle(ws.a[0].device)
+            if schedule == "stealing":
+                queue = torch.zeros(_native.QUEUE_BYTES // 4, dtype=torch.int32, device="cuda")
+                status = _native.library().moegemm_grouped_gemm_stealing(*args, queue.data_ptr(), stream)
+            else:
+                status = _native.library().moegemm_grouped_gemm(*args, stream)
             _native.check(status)
             torch.cuda.synchronize()
+            if schedule == "stealing":
+                assert not queue.any(), f"queue not re-armed: {queue.tolist()}"
             for e, ((storage, lead), ref) in enumerate(zip(storages, expected)):
-                label = f"k {k} tile {(bm, bn, bk, warps, stages)} grid {grid} problem {e}"
+                label = f"{schedule} k {k} tile {(bm, bn, bk, warps, stages)} grid {grid} problem {e}"
                 assert torch.equal(ws.c[e], ref), label
                 assert torch.isnan(storage[:lead]).all() and torch.isnan(storage[lead + m * n:]).all(), label
