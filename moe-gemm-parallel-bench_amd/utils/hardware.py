@@ -31,7 +31,11 @@ from typing import Any
 
 
 def _run(args: list[str]) -> str | None:
-    """stdout of a short tool call, or None when the tool is absent, fails or hangs."""
+    """stdout of a short tool call, or None when the tool is absent, fails or hangs.  Skipped under a
+    profiler's preloaded library (rocprofv3): the child would load it too, and profiling the tool
+    is not wanted."""
+    if "rocprof" in os.environ.get("LD_PRELOAD", ""):
+        return None
     try:
         done = subprocess.run(args, capture_output=True, text=True, timeout=15, check=False)
     except (OSError, subprocess.SubprocessError):
