@@ -673,6 +673,7 @@ struct FastTile {
   // 64x512x64 gained 8 % at K = 256 (4 slices) and lost 2-3 % at K = 2048 (32 slices).
   static constexpr bool CHAIN_OK = STAGES == 2 && FM * FN * ACC <= 128 && BM * BN <= 32768;
   static constexpr int CHAIN_MAX_SLICES = FM * FN * ACC <= 64 ? (1 << 30) : 8;
+  static constexpr bool CHAIN_STEALING = true;  // the chained loop also runs the stealing schedule
   static constexpr int CH_ROWS_FIT = STAGED_OK ? (XMIN * 1024 / ROWB) / MI * MI : MI;
   static constexpr int CH_ROWS = CH_ROWS_FIT < WTM ? CH_ROWS_FIT : WTM;  // staged rows per round
   static constexpr int CHAIN_STORES = STAGED_OK ? WTM * ROWB / 1024 : FM * FN * (ACC / 4);

@@ -276,7 +276,8 @@ struct GemmTile {
   static constexpr int PREFIX_OFFSET = 2 * STAGE_BYTES;
   static constexpr int LDS_BYTES = PREFIX_OFFSET + (PREFIX + 1) * 4 + NT * 4;
   static constexpr int WAVES_PER_EU = 1;
-  static constexpr bool CHAIN_OK = false;  // no cross-tile copy chaining (FastTile only)
+  static constexpr bool CHAIN_OK = false;  // no cross-tile copy chaining (LDS-DMA tiles only)
+  static constexpr bool CHAIN_STEALING = false;
 
   static_assert(BM % WM == 0 && BN % WN == 0, "tile must split evenly over waves");
   static_assert(WTM % MI == 0 && WTN % MI == 0, "wave tile must be a multiple of the MFMA tile");
@@ -804,7 +805,7 @@ grouped_gemm_kernel(KParams p) {
   // out.
   if constexpr (T::CHAIN_OK) {
     if (splits == 1 && !p.swiglu && (p.mode == MODE_SINGLE || p.mode == MODE_HOMOGENEOUS) &&
-        (p.K + T::BK - 1) / T::BK <= T::CHAIN_MAX_SLICES) {
+        (!stealing || T::CHAIN_STEALING) && (p.K + T::BK - 1) / T::BK <= T::CHAIN_MAX_SLICES) {
       auto describe = [&](int unit, ProblemDesc& pd, int& tm, int& tn) {
         simple_tile<T>(p, unit, pd, tm, tn);
         pd.swiglu = 0;

@@ -110,6 +110,144 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
       Base::store_tile(acc, pd, m0, n0, wave_m, wave_n, smem);
     }
   }
+
+  // Cross-tile chaining on the static schedule of single and homogeneous launches.  A tile's last
+  // three memory phases would refill their buffers with zero slices past K; instead they copy the
+  // next tile's slices 0..2 (each wave into its own slots, as always).  C then leaves through the
+  // wave's slots of the last slice's buffer, in CHAIN_STORES counted stores
+  // (FastTile::staged_store_counted): group 1 read that slice in its memory phase before the
+  // barrier that ends group 0's last compute phase, so both groups may stage there.  After its
+  // stores each wave copies the next tile's slice 3 into the same slots (its staging reads have
+  // returned: the stores consumed them).  A wave's vector memory operations complete in issue
+  // order, so the next tile waits for slice 0 with 3 * XMIN + CHAIN_STORES younger operations
+  // outstanding, and for slices 1 and 2 with the stores still counted; only slice 3's wait
+  // (end of the memory or compute phase of K step 2) needs the stores done.  The next tile's buffers
+  // rotate by K slices.  Tiles of fewer than STAGES slices, the last tile, and C that is not
+  // 16-byte aligned run the unchained epilogue (zero slices, wait for every copy).  The next unit
+  // is computed right after the prologue barrier: only the static schedule is served here.
+  static constexpr bool CHAIN_OK = Base::STAGED_OK && (STAGES & (STAGES - 1)) == 0;
+  static constexpr int CHAIN_MAX_SLICES = 1 << 30;
+  static constexpr bool CHAIN_STEALING = false;
+  static constexpr int CHAIN_STORES = Base::CHAIN_STORES;
+  static_assert(!CHAIN_OK || 3 * XMIN + CHAIN_STORES < 64, "outstanding operations must fit the 6-bit vmcnt");
+  static_assert(!CHAIN_OK || (Base::CH_ROWS > 0 && Base::WTM % Base::CH_ROWS == 0 &&
+                              (Base::CH_ROWS * Base::ROWB) % 1024 == 0),
+                "staging rounds must cover the wave tile in whole slots of one stage");
+  using Chain = typename Base::Chain;
+
+  template <class Sched>
+  __device__ static __forceinline__ bool run_tile_chained(const ProblemDesc& pd, int tm, int tn, char* smem, Chain& ch,
+                                                          Sched& sched, ProblemDesc& next, int& ntm, int& ntn) {
+    static_assert(CHAIN_OK, "the chained epilogue stages C in one stage's slots");
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int wave_m = wave / WN, wave_n = wave % WN;
+    const bool second = wave >= NW / 2;
+    const int m0 = tm * BM, n0 = tn * BN;
+    Dma d;
+    Base::setup_dma(d, pd, m0, n0, smem);
+
+    acc_t acc[FM][FN];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int i = 0; i < ACC; ++i) acc[fm][fn][i] = 0.0f;
+
+    const bool pre = ch.prefetched;
+    const int rot = pre ? ch.rot : 0;
+    if (pre) {
+      // Issued by the previous tile: slices 0, 1, 2, then its CHAIN_STORES stores, then slice 3.
+      wait_vmcnt<3 * XMIN + CHAIN_STORES>();
+    } else {
+#pragma unroll
+      for (int s = 0; s < STAGES; ++s) Base::issue_stage(d, s, s * BK);
+      wait_vmcnt<(STAGES - 1) * XMIN>();
+    }
+    phase_barrier();
+    if (second) phase_barrier();  // group 1 runs one barrier behind
+    sched.started();
+    const bool has_next = sched.next(next, ntm, ntn);
+    const int kt_count = (pd.k + BK - 1) / BK;
+    const bool c16 = ((reinterpret_cast<uintptr_t>(pd.c) & 15) == 0) && (pd.scm & 7) == 0;
+    const bool chain = has_next && kt_count >= STAGES && c16;
+
+    // One K step.  ISSUE: 0 none (kt = 0), 1 this tile's slice kt + STAGES - 1 (zeros past K),
+    // 2 chosen at run time (the next tile's slices once that index passes K).  GENERIC: the wait for
+    // slice kt + 1 depends on kt (stores of the previous tile still counted, no successor).  The
+    // steady-state steps (ISSUE 1, fixed wait) carry no branches.
+    i16x8_t af[KK][FM], bf[KK][FN];
+    auto step = [&](int kt, auto issue_kind, auto generic) {
+      constexpr int ISSUE = decltype(issue_kind)::value;
+      constexpr bool GENERIC = decltype(generic)::value;
+      // Memory phase.
+      const char* cur = smem + ((kt + rot) & (STAGES - 1)) * STAGE_BYTES;
+      const int buf = (kt - 1 + rot) & (STAGES - 1), s = kt - 1 + STAGES;
+      if constexpr (ISSUE == 1) {
+        Base::issue_stage(d, buf, s * BK);
+      } else if constexpr (ISSUE == 2) {
+        if (chain && s >= kt_count) {
+          Dma dn;  // the next tile's copy state, recomputed for each of its first slices
+          Base::setup_dma(dn, next, ntm * BM, ntn * BN, smem);
+          Base::issue_stage(dn, buf, (s - kt_count) * BK);
+        } else {
+          Base::issue_stage(d, buf, s * BK);
+        }
+      }
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk)
+        Base::load_frags(af[kk], bf[kk], cur, cur + A_BYTES, kk, wave_m, wave_n, false);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      // Slice kt + 1 complete (the chained last slice has no successor in this tile).
+      auto wait_next = [&] {
+        if constexpr (GENERIC) {
+          if (!chain || kt + 1 < kt_count) {
+            if (pre && kt < 2) wait_vmcnt<(STAGES - 2) * XMIN + CHAIN_STORES>();
+            else wait_vmcnt<(STAGES - 2) * XMIN>();
+          }
+        } else {
+          wait_vmcnt<(STAGES - 2) * XMIN>();
+        }
+      };
+      if (second) wait_next();
+      phase_barrier();
+      // Compute phase.
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) Base::template mfma_rows<0, FM>(acc, af[kk], bf[kk]);
+      if (!second) wait_next();
+      phase_barrier();
+    };
+    using no_issue = std::integral_constant<int, 0>;
+    using own_issue = std::integral_constant<int, 1>;
+    using any_issue = std::integral_constant<int, 2>;
+    step(0, no_issue{}, std::true_type{});
+    int kt = 1;
+    for (; kt < 2 && kt < kt_count; ++kt) step(kt, any_issue{}, std::true_type{});
+    for (; kt + STAGES - 1 < kt_count; ++kt) step(kt, own_issue{}, std::false_type{});
+    for (; kt < kt_count; ++kt) step(kt, any_issue{}, std::true_type{});
+    if (chain) {
+      const int last = (kt_count - 1 + rot) & (STAGES - 1);
+      Base::staged_store_counted(acc, pd, m0, n0, wave_m, wave_n, smem, last);
+      {
+        Dma dn;
+        Base::setup_dma(dn, next, ntm * BM, ntn * BN, smem);
+        Base::issue_stage(dn, last, (STAGES - 1) * BK);
+      }
+      if (!second) phase_barrier();
+      ch.rot = (kt_count + rot) & (STAGES - 1);
+      ch.prefetched = true;
+    } else {
+      wait_vmcnt<0>();
+      if (!second) {
+        Base::store_tile(acc, pd, m0, n0, wave_m, wave_n, smem);
+        phase_barrier();
+      } else {
+        Base::store_tile(acc, pd, m0, n0, wave_m, wave_n, smem);
+      }
+      ch.prefetched = false;
+    }
+    return has_next;
+  }
 };
 
 }  // namespace moegemm

@@ -155,3 +155,57 @@ def test_chained_two_stage_tiles_every_k_slice_count(k, schedule):
                 label = f"{schedule} k {k} tile {(bm, bn, bk, warps, stages)} grid {grid} problem {e}"
                 assert torch.equal(ws.c[e], ref), label
                 assert torch.isnan(storage[:lead]).all() and torch.isnan(storage[lead + m * n:]).all(), label
+
+
+@pytest.mark.parametrize("schedule", ["static", "stealing"])
+@pytest.mark.parametrize("k", [64, 96, 128, 136, 160, 232])
+def test_chained_ping_pong_tiles_every_k_slice_count(k, schedule):
+    """The 8-wave 256x256 ping-pong tiles chain across tiles on the static schedule: a tile's last
+    three memory phases copy the next tile's first slices, C leaves through one stage, and the next
+    tile's first waits count the previous tile's stores.  K from two slices (unchained) through
+    four (the first chained count) to several with a tail; several tiles per workgroup, ragged M
+    and N, C alternating 16- and 8-byte alignment (8-byte aligned C runs the unchained epilogue, so
+    chained and unchained tiles alternate in one workgroup).  The stealing schedule runs these
+    tiles unchained.  Exact integers, intact guard bands, re-armed queue."""
+    from kernels import _native
+    from kernels.grouped_gemm import build_grouped_workspace
+
+    dtype = torch.bfloat16
+    groups, m, n = 4, 300, 520
+    ws = build_grouped_workspace([(m, k, n)] * groups, dtype, seed=3)
+    storages = []
+    for e in range(groups):
+        ws.a[e].copy_(_ints((m, k), dtype))
+        ws.b[e].copy_(_ints((k, n), dtype))
+        lead = GUARD + (4 if e % 3 == 1 else 0)
+        storage = torch.full((lead + m * n + GUARD,), float("nan"), device="cuda", dtype=dtype)
+        ws.c[e] = storage[lead:lead + m * n].view(m, n)
+        ws.c_ptrs[e] = ws.c[e].data_ptr()
+        storages.append((storage, lead))
+    code = _native.dtype_code(dtype)
+    expected = [(a.double() @ b.double()).to(dtype) for a, b, _ in ws.problem_tensors()]
+    ping_pong = [t for t in _tiles(dtype) if t[:2] == (256, 256) and t[3] == 8 and t[4] >= 3]
+    assert ping_pong
+    for bm, bn, bk, warps, stages in ping_pong:
+        tiles = groups * -(-m // bm) * -(-n // bn)
+        for grid in (1, 5, 8):
+            print(f"ping-pong chained {schedule} k={k} tile={(bm, bn, bk, warps, stages)} tiles={tiles} grid={grid}",
+                  flush=True)
+            for storage, _ in storages:
+                storage.fill_(float("nan"))
+            args = (ws.a_ptrs.data_ptr(), ws.b_ptrs.data_ptr(), ws.c_ptrs.data_ptr(), ws.dims.data_ptr(),
+                    ws.strides.data_ptr(), groups, m, n, k, 1, tiles, code, 0, bm, bn, bk, 4, warps, stages, grid, 1)
+            stream = _native.current_stream_handle(ws.a[0].device)
+            if schedule == "stealing":
+                queue = torch.zeros(_native.QUEUE_BYTES // 4, dtype=torch.int32, device="cuda")
+                status = _native.library().moegemm_grouped_gemm_stealing(*args, queue.data_ptr(), stream)
+            else:
+                status = _native.library().moegemm_grouped_gemm(*args, stream)
+            _native.check(status)
+            torch.cuda.synchronize()
+            if schedule == "stealing":
+                assert not queue.any(), f"queue not re-armed: {queue.tolist()}"
+            for e, ((storage, lead), ref) in enumerate(zip(storages, expected)):
+                label = f"{schedule} k {k} tile {(bm, bn, bk, warps, stages)} grid {grid} problem {e}"
+                assert torch.equal(ws.c[e], ref), label
+                assert torch.isnan(storage[:lead]).all() and torch.isnan(storage[lead + m * n:]).all(), label
