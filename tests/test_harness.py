@@ -240,3 +240,32 @@ def test_compare_arguments_and_default_cases():
     moe = dict(comparison_cases(args, 256))
     assert list(moe) == ["W1_EP_M8", "W1_TP_M8", "W2_EP_M8", "W2_TP_M8"]
     assert math.prod(moe["W2_TP_M8"][0]) == 8 * 256 * 7168
+
+
+def test_power_harness_parses_amd_smi_and_kernel_config():
+    """harness.power reads SOCKET_POWER and every XCD's GFX clock from amd-smi's text output, and
+    takes --kernel-config in bench.py's order (BM,BN,BK,WARPS,STAGES,GROUP_M,MULT)."""
+    from harness.power import parse_amd_smi, parse_kernel_config
+
+    text = """GPU: 0
+    POWER:
+        SOCKET_POWER: 1399 W
+        GFX_VOLTAGE: N/A
+    CLOCK:
+        GFX_0:
+            CLK: 1456 MHz
+            MIN_CLK: 500 MHz
+        GFX_1:
+            CLK: 1470 MHz
+            MIN_CLK: 500 MHz
+        MEM_0:
+            CLK: 1900 MHz
+"""
+    power, clocks = parse_amd_smi(text)
+    assert power == 1399.0
+    assert clocks == [1456.0, 1470.0]
+    assert parse_amd_smi("") == (None, [])
+    cfg = parse_kernel_config("256,256,32,8,4,8,1")
+    assert (cfg.block_m, cfg.block_n, cfg.block_k, cfg.num_warps, cfg.num_stages, cfg.group_size_m,
+            cfg.cta_multiplier) == (256, 256, 32, 8, 4, 8, 1)
+    assert parse_kernel_config(None) is None
