@@ -209,3 +209,55 @@ def test_chained_ping_pong_tiles_every_k_slice_count(k, schedule):
                 label = f"{schedule} k {k} tile {(bm, bn, bk, warps, stages)} grid {grid} problem {e}"
                 assert torch.equal(ws.c[e], ref), label
                 assert torch.isnan(storage[:lead]).all() and torch.isnan(storage[lead + m * n:]).all(), label
+
+
+@pytest.mark.parametrize("k", [64, 128, 136, 232])
+def test_ping_pong_swiglu_several_tiles_per_workgroup(k):
+    """The packed W13 SwiGLU epilogue on the ping-pong tiles with several tiles per workgroup
+    stores bit for bit what one tile per workgroup stores, keeps the guard bands around every H
+    intact, and matches the oracle's SwiGLU within the normwise bound.  (SwiGLU launches run
+    these tiles unchained: chaining them measured no gain.)"""
+    import numpy as np
+
+    from helpers import from_oracle, normwise, to_oracle
+    from kernels import _native
+    from kernels.grouped_gemm import build_fused_gate_up_workspace
+    from oracle import oracle
+
+    dtype = torch.bfloat16
+    groups, m, f = 4, 300, 264
+    n = 2 * f
+    ws = build_fused_gate_up_workspace([(m, k, n)] * groups, dtype, seed=4)
+    storages = []
+    for e in range(groups):
+        ws.a[e].copy_(_ints((m, k), dtype))
+        ws.b[e].copy_(_ints((k, n), dtype))
+        lead = GUARD + (4 if e % 2 else 0)  # odd problems: H only 8-byte aligned
+        storage = torch.full((lead + m * f + GUARD,), float("nan"), device="cuda", dtype=dtype)
+        storages.append((storage, lead))
+    h_ptrs = torch.tensor([s[lead:].data_ptr() for s, lead in storages], device="cuda", dtype=torch.int64)
+    code = _native.dtype_code(dtype)
+    ping_pong = [t for t in _tiles(dtype) if t[:2] == (256, 256) and t[3] == 8 and t[4] >= 3]
+    assert ping_pong
+    for bm, bn, bk, warps, stages in ping_pong:
+        tiles = groups * -(-m // bm) * -(-f // (bn // 2))
+        results = {}
+        for grid in (tiles, 1, 5, 8):
+            print(f"ping-pong swiglu k={k} tile={(bm, bn, bk, warps, stages)} tiles={tiles} grid={grid}", flush=True)
+            for storage, _ in storages:
+                storage.fill_(float("nan"))
+            status = _native.library().moegemm_grouped_gemm_swiglu(
+                ws.a_ptrs.data_ptr(), ws.b_ptrs.data_ptr(), h_ptrs.data_ptr(), ws.dims.data_ptr(),
+                ws.strides.data_ptr(), groups, m, n, k, 1, tiles, code, bm, bn, bk, 4, warps, stages, grid, 1,
+                _native.current_stream_handle(ws.a[0].device))
+            _native.check(status)
+            torch.cuda.synchronize()
+            results[grid] = [s[lead:lead + m * f].clone() for s, lead in storages]
+            for e, (storage, lead) in enumerate(storages):
+                label = f"k {k} tile {(bm, bn, bk, warps, stages)} grid {grid} problem {e}"
+                assert torch.isnan(storage[:lead]).all() and torch.isnan(storage[lead + m * f:]).all(), label
+                assert torch.equal(results[grid][e], results[tiles][e]), label
+        for e in (0, groups - 1):
+            ref = from_oracle(oracle.swiglu_reference(np.ascontiguousarray(to_oracle(ws.a[e])),
+                                                      np.ascontiguousarray(to_oracle(ws.b[e])), "bf16"), "bf16")
+            assert normwise(results[tiles][e].view(m, f).cpu(), ref) <= 1e-2, f"k {k} problem {e}"
