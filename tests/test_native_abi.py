@@ -4,6 +4,7 @@ and rejects bad arguments with the documented codes before any GPU work."""
 from __future__ import annotations
 
 import ctypes
+import math
 import re
 from pathlib import Path
 
@@ -39,6 +40,18 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert lib.moegemm_abi_version() == _native.ABI_VERSION
     header_version = int(re.search(r"#define MOEGEMM_ABI_VERSION (\d+)", HEADER.read_text()).group(1))
     assert header_version == _native.ABI_VERSION
+
+
+def test_buffer_sizes_agree_between_header_and_binding():
+    """The caller-allocated stealing queue and the no-alloc scratch limit have one size in C and Python."""
+    text = HEADER.read_text()
+    queue = int(re.search(r"#define MOEGEMM_QUEUE_BYTES (\d+)", text).group(1))
+    assert queue == _native.QUEUE_BYTES
+    assert queue % 256 == 0 and queue >= 17 * 256  # 17 counters, one per 256-byte block
+    scratch = re.search(r"#define MOEGEMM_NOALLOC_SCRATCH_BYTES \(([^)]*)\)", text).group(1)
+    assert re.fullmatch(r"[0-9 *+]+", scratch), scratch
+    total = sum(math.prod(int(f) for f in term.split("*")) for term in scratch.split("+"))
+    assert total == _native.NOALLOC_SCRATCH_BYTES
 
 
 def test_compiled_menus_match_python_candidate_pools():
