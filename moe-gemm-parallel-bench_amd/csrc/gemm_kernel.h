@@ -616,15 +616,16 @@ __device__ __forceinline__ void load_prefix(const KParams& p, int* s_pref, int* 
 // on XCD b % 8 (round-robin dispatch) and XCD x owns units [lo(x), lo(x + 1)) — a contiguous run,
 // so the tiles sharing an expert's B panel stay in one XCD's L2; otherwise one queue owns all
 // units.  The `per` workgroups of an XCD take their first units statically (lo(x) + b / 8) and
-// draw later ones from ticket counter queue[x] (ticket c is unit lo(x) + per + c).  The ticket for
+// draw later ones from ticket counter x (ticket c is unit lo(x) + per + c).  The ticket for
 // the next unit is drawn after the current tile's K loop, before its C stores: vector memory
 // operations complete in issue order, so an atomic issued earlier would hold up the tile's copy
 // waits, while here its latency overlaps the epilogue.  When a queue is drained, wave 0 reads all
 // counters at once (one lane each) and moves to the queue with the most units left, so units left
 // on a slow XCD are taken by idle ones and a drained workgroup learns that every queue is empty in
-// one round trip.  Every workgroup counts itself out in queue[kQueues] after its last claim has
-// returned, and the last one re-arms all counters to zero for the next launch.  Chained two-stage
-// tiles draw one unit further ahead (see the chained loop of grouped_gemm_kernel).
+// one round trip.  Every workgroup counts itself out after its last claim has returned (two-level
+// exit counts, below), and the last one re-arms all counters to zero for the next launch.  Chained
+// two-stage tiles draw their ticket earlier, right after the tile's first copies, where the wave's
+// next wait is for every copy anyway (see the chained loop of grouped_gemm_kernel).
 constexpr int kQueues = 8;
 // Counters of the queue buffer, each in a 256-byte block of its own (int32 index = slot *
 // kQueueStride): tickets of queue y in slot y, the exit count of the workgroups b with b % 8 == x
