@@ -683,6 +683,39 @@ struct TileQueue {
   }
 };
 
+// Problem and tile coordinates of tile t in a generic or offsets launch (unsplit fields only).  The
+// loaded prefix chunk (s_pref, problems chunk_first ..) must cover t: s_pref[0] <= t < s_pref[PREFIX].
+template <class T>
+__device__ __forceinline__ void searched_tile(const KParams& p, const int* s_pref, int chunk_first, int t,
+                                              ProblemDesc& pd, int& tm, int& tn) {
+  int lo = 0, hi = T::PREFIX;  // largest i with s_pref[i] <= t
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (s_pref[mid] <= t) lo = mid; else hi = mid;
+  }
+  const int e = uniform(chunk_first + lo);
+  const int local = uniform(t - s_pref[lo]);
+  if (p.mode == MODE_OFFSETS) {
+    int m;
+    const int row0 = uniform(offsets_rows(p, e, m));
+    pd.m = uniform(m); pd.n = p.N; pd.k = p.K;
+    pd.sam = p.sam; pd.sak = 1; pd.sbk = p.sbk; pd.sbn = 1; pd.scm = p.scm; pd.scn = 1;
+    constexpr int ES = T::ES;
+    pd.a = static_cast<const char*>(p.a) + (int64_t)row0 * p.sam * ES;
+    pd.b = static_cast<const char*>(p.b) + (int64_t)e * p.sbg * ES;
+    pd.c = static_cast<char*>(p.c) + (int64_t)row0 * p.scm * ES;
+  } else {
+    pd.m = p.dims[e * 3 + 0]; pd.n = p.dims[e * 3 + 1]; pd.k = p.dims[e * 3 + 2];
+    const int64_t* s = p.strides + (int64_t)e * 6;
+    pd.sam = s[0]; pd.sak = s[1]; pd.sbk = s[2]; pd.sbn = s[3]; pd.scm = s[4]; pd.scn = s[5];
+    pd.a = reinterpret_cast<const char*>(p.a_ptrs[e]);
+    pd.b = reinterpret_cast<const char*>(p.b_ptrs[e]);
+    pd.c = reinterpret_cast<char*>(p.c_ptrs[e]);
+  }
+  const int mt = (pd.m + T::BM - 1) / T::BM, nt = (pd.n + T::BN - 1) / T::BN;
+  group_m_order(local, mt, nt, p.group_m, tm, tn);
+}
+
 // The three schedule hooks of FastTile::run_tile_chained, as one object.
 template <class BeforeBarrier, class Next, class Started>
 struct ChainHooks {
@@ -794,21 +827,27 @@ grouped_gemm_kernel(KParams p) {
       }
     }
   };
-  // Two-stage tiles of single and homogeneous launches chain their copies across tiles
-  // (FastTile::run_tile_chained): each tile issues the next unit's first K slice at the boundary
-  // before its last slice, so the next unit must be known by then.  The static schedule knows it in
-  // advance.  Under work stealing, lane 0 of wave 0 draws the ticket for the next unit once the
-  // tile's slice-1 copies are issued, and wave 0 resolves it at the tile's first slice boundary,
-  // before the barrier that publishes it to the workgroup.  Each tile claims exactly its successor,
-  // as the unchained loop does, only earlier: a workgroup never holds more than one unit ahead, so
-  // the last units of a queue still go to whichever workgroups reach them first.  Every ticket is
-  // resolved within the tile that drew it, so none is outstanding when the workgroup counts itself
-  // out.
+  // CHAIN_OK tiles (two-stage FastTiles, the ping-pong tile) chain their copies across tiles in
+  // single, homogeneous and offsets launches; offsets launches only when their groups fit the one
+  // prefix chunk loaded above, so locating a tile needs no workgroup barrier.  A tile issues the
+  // next unit's first K slices before its own last ones (FastTile::run_tile_chained,
+  // PingPongTile::run_tile_chained), so the next unit must be known by then.  The static schedule
+  // knows it in advance.  Under work stealing (two-stage FastTiles only), lane 0 of wave 0 draws the
+  // ticket for the next unit once the tile's slice-1 copies are issued, and wave 0 resolves it at
+  // the tile's first slice boundary, before the barrier that publishes it to the workgroup.  Each
+  // tile claims exactly its successor, as the unchained loop does, only earlier: a workgroup never
+  // holds more than one unit ahead, so the last units of a queue still go to whichever workgroups
+  // reach them first.  Every ticket is resolved within the tile that drew it, so none is
+  // outstanding when the workgroup counts itself out.
   if constexpr (T::CHAIN_OK) {
-    if (splits == 1 && !p.swiglu && (p.mode == MODE_SINGLE || p.mode == MODE_HOMOGENEOUS) &&
+    if (splits == 1 && !p.swiglu &&
+        (p.mode == MODE_SINGLE || p.mode == MODE_HOMOGENEOUS || (p.mode == MODE_OFFSETS && p.G <= T::PREFIX)) &&
         (!stealing || T::CHAIN_STEALING) && (p.K + T::BK - 1) / T::BK <= T::CHAIN_MAX_SLICES) {
       auto describe = [&](int unit, ProblemDesc& pd, int& tm, int& tn) {
-        simple_tile<T>(p, unit, pd, tm, tn);
+        if (p.mode == MODE_OFFSETS)
+          searched_tile<T>(p, s_pref, 0, unit, pd, tm, tn);
+        else
+          simple_tile<T>(p, unit, pd, tm, tn);
         pd.swiglu = 0;
         pd.splits = 1;
         pd.split = 0;
@@ -888,32 +927,7 @@ grouped_gemm_kernel(KParams p) {
         next_unit(-1);
         continue;
       }
-      int lo = 0, hi = T::PREFIX;           // largest i with s_pref[i] <= t
-      while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (s_pref[mid] <= t) lo = mid; else hi = mid;
-      }
-      const int e = uniform(chunk_first + lo);
-      const int local = uniform(t - s_pref[lo]);
-      if (p.mode == MODE_OFFSETS) {
-        int m;
-        const int row0 = uniform(offsets_rows(p, e, m));
-        pd.m = uniform(m); pd.n = p.N; pd.k = p.K;
-        pd.sam = p.sam; pd.sak = 1; pd.sbk = p.sbk; pd.sbn = 1; pd.scm = p.scm; pd.scn = 1;
-        constexpr int ES = T::ES;
-        pd.a = static_cast<const char*>(p.a) + (int64_t)row0 * p.sam * ES;
-        pd.b = static_cast<const char*>(p.b) + (int64_t)e * p.sbg * ES;
-        pd.c = static_cast<char*>(p.c) + (int64_t)row0 * p.scm * ES;
-      } else {
-        pd.m = p.dims[e * 3 + 0]; pd.n = p.dims[e * 3 + 1]; pd.k = p.dims[e * 3 + 2];
-        const int64_t* s = p.strides + (int64_t)e * 6;
-        pd.sam = s[0]; pd.sak = s[1]; pd.sbk = s[2]; pd.sbn = s[3]; pd.scm = s[4]; pd.scn = s[5];
-        pd.a = reinterpret_cast<const char*>(p.a_ptrs[e]);
-        pd.b = reinterpret_cast<const char*>(p.b_ptrs[e]);
-        pd.c = reinterpret_cast<char*>(p.c_ptrs[e]);
-      }
-      const int mt = (pd.m + T::BM - 1) / T::BM, nt = (pd.n + T::BN - 1) / T::BN;
-      group_m_order(local, mt, nt, p.group_m, tm, tn);
+      searched_tile<T>(p, s_pref, chunk_first, t, pd, tm, tn);
     }
     pd.swiglu = p.swiglu;
     pd.splits = splits;

@@ -237,3 +237,53 @@ def test_dsv3_lognormal_routing_exact_and_oracle(schedule, mean):
         r0, r1 = (offs_list[e - 1] if e else 0), offs_list[e]
         if r1 > r0:
             assert torch.equal(out[r0:r1], torch.full_like(out[r0:r1], float(k * (e % 31 + 1)))), f"expert {e}"
+
+
+@pytest.mark.parametrize("schedule", ["static", "stealing"])
+@pytest.mark.parametrize("k", [64, 136, 328])
+def test_chained_tiles_on_ragged_offsets_small_grids(k, schedule):
+    """Offsets launches whose groups fit one prefix chunk run the chained schedule: every chained
+    tile (two-stage tiles up to 64 rows, the ping-pong tile), at grids that give each workgroup many
+    ragged tiles, empty groups included, rows past the last offset left untouched, static and
+    stealing.  A is small integers and each group's B is a constant, so every row's exact value is
+    known: k * sum(A row) * b_e, here with A = 1 and b_e = e % 7 + 1."""
+    from kernels import _native
+
+    sizes = [70, 0, 3, 130, 257, 0, 1, 64, 200, 9]
+    ends = list(np.cumsum(sizes))
+    groups, rows, n = len(sizes), int(ends[-1]), 392
+    spare = 5  # rows past the last offset: never written
+    mat_a = torch.ones((rows + spare, k), device="cuda", dtype=torch.bfloat16)
+    mat_b = torch.stack([torch.full((k, n), float(e % 7 + 1), device="cuda", dtype=torch.bfloat16)
+                         for e in range(groups)])
+    offs = torch.tensor(ends, device="cuda", dtype=torch.int32)
+    expected = torch.full((rows + spare, n), float("nan"), dtype=torch.float64)
+    prev = 0
+    for e, end in enumerate(ends):
+        expected[prev:end] = float(k * (e % 7 + 1))
+        prev = end
+    expected = expected.to(torch.bfloat16)
+    chained = [t for t in _native.compiled_kernels(_native.DTYPE_BF16)
+               if (t[4] == 2 and t[0] <= 64) or (t[:2] == (256, 256) and t[3] == 8 and t[4] >= 3)]
+    assert chained
+    for bm, bn, bk, warps, stages, *_ in chained:
+        for grid in (1, 5, 8):
+            print(f"offsets chained {schedule} k={k} tile={(bm, bn, bk, warps, stages)} grid={grid}", flush=True)
+            out = torch.full((rows + spare, n), float("nan"), device="cuda", dtype=torch.bfloat16)
+            args = (mat_a.data_ptr(), mat_b.data_ptr(), out.data_ptr(), offs.data_ptr(), groups, rows, n, k,
+                    mat_a.stride(0), mat_b.stride(0), mat_b.stride(1), out.stride(0), _native.DTYPE_BF16, 0,
+                    bm, bn, bk, 4, warps, stages, grid)
+            stream = _native.current_stream_handle(mat_a.device)
+            if schedule == "stealing":
+                queue = torch.zeros(_native.QUEUE_BYTES // 4, dtype=torch.int32, device="cuda")
+                status = _native.library().moegemm_grouped_mm_offs_stealing(*args, queue.data_ptr(), stream)
+            else:
+                status = _native.library().moegemm_grouped_mm_offs(*args, stream)
+            _native.check(status)
+            torch.cuda.synchronize()
+            if schedule == "stealing":
+                assert not queue.any(), f"queue not re-armed: {queue.tolist()}"
+            label = f"{schedule} k {k} tile {(bm, bn, bk, warps, stages)} grid {grid}"
+            got = out.cpu()
+            assert torch.equal(got[:rows], expected[:rows]), label
+            assert torch.isnan(got[rows:]).all(), label
