@@ -7,7 +7,8 @@
   with its ring tuner, on small EP/TP per-rank shapes;
 * the comparison runner against the per-expert hipBLASLt loop (NaN-poisoned, checked candidates,
   two reversed rounds), and its verdict on a contender that writes nothing;
-* the torch grouped_mm provider: admitted or not by its trace check, its results are right.
+* the torch grouped_mm provider: admitted or not by its trace check, its results are right;
+* the power probe: a short pinned run prints one table row per workload.
 """
 
 from __future__ import annotations
@@ -147,3 +148,18 @@ def test_torch_grouped_mm_provider_results_whether_or_not_admitted():
     torch.cuda.synchronize()
     for a, b, c in workspace.problem_tensors():
         torch.testing.assert_close(c.float(), a.float() @ b.float(), rtol=2e-2, atol=2e-2)
+
+
+def test_power_probe_prints_a_row_per_workload(capsys):
+    """harness.power, shortened: the pinned grouped and single workloads each print a table row with
+    a positive rate (power and clock read "n/a" where amd-smi is absent)."""
+    from harness.power import main
+
+    assert main(["--seconds", "1", "--skip", "0.3", "--pause", "0", "--workloads", "grouped,single",
+                 "--kernel-config", "256,256,32,8,4,8,1"]) == 0
+    rows = [line for line in capsys.readouterr().out.splitlines() if line.startswith("| grouped") or
+            line.startswith("| single")]
+    assert len(rows) == 2, rows
+    for row in rows:
+        cells = [c.strip() for c in row.strip("|").split("|")]
+        assert float(cells[1]) > 0 and float(cells[2]) > 0, row
