@@ -18,6 +18,7 @@ This project's launches use the autotuned config unless ``--kernel-config`` pins
 from __future__ import annotations
 
 import argparse
+import os
 import re
 import subprocess
 import threading
@@ -51,6 +52,9 @@ class Sampler:
         self._thread = threading.Thread(target=self._run, daemon=True)
 
     def _run(self) -> None:
+        # Under a profiler's preloaded library (rocprofv3) the tool would run under it too: no samples.
+        if "rocprof" in os.environ.get("LD_PRELOAD", ""):
+            return
         while not self._stop.is_set():
             try:
                 out = subprocess.run(["amd-smi", "metric", "--power", "--clock"], capture_output=True,
