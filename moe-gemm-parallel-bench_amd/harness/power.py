@@ -94,7 +94,7 @@ def sustained(step, seconds: float, skip: float, chunk: int = 20) -> tuple[float
         end.record()
         end.synchronize()
         rates.append((time.time(), start.elapsed_time(end) / chunk))
-    late = [ms for t, ms in rates if t > t0 + skip]
+    late = [ms for t, ms in rates if t > t0 + skip] or [ms for _, ms in rates]  # all, if skip >= seconds
     return sum(late) / len(late), t0 + skip, time.time()
 
 
