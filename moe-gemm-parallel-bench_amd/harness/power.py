@@ -10,7 +10,9 @@ Workloads (bf16, seeded inputs):
 
 * ``grouped``: DSV3 EP W13 at M_e=512, 32 x [512,7168]@[7168,4096] (the bench.py headline);
 * ``single``: one [16384,7168]@[7168,4096] GEMM with the same FLOPs, this project's kernel;
-* ``hipblaslt``: the same single GEMM through ``torch.mm`` (hipBLASLt on ROCm).
+* ``hipblaslt``: the same single GEMM through ``torch.mm`` (hipBLASLt on ROCm);
+* ``decode``: DSV3 EP W13 at M_e=8, 32 x [8,7168]@[7168,4096] (HBM-bound; its rate is reported in
+  TFLOP/s like the others, and its bytes per launch are 2 B x 32 x (8*7168 + 7168*4096 + 8*4096)).
 
 This project's launches use the autotuned config unless ``--kernel-config`` pins one.
 """
@@ -29,8 +31,9 @@ import torch
 from kernels.grouped_gemm import build_grouped_workspace, launch_grouped
 from kernels.matmul import KernelConfig, launch_matmul
 
-WORKLOADS = ("grouped", "single", "hipblaslt")
+WORKLOADS = ("grouped", "single", "hipblaslt", "decode")
 GROUPED_SHAPE = (512, 7168, 4096)  # (M_e, K, N) per expert
+DECODE_SHAPE = (8, 7168, 4096)
 EXPERTS = 32
 SINGLE_SHAPE = (16384, 7168, 4096)
 
@@ -112,7 +115,7 @@ def main(argv=None) -> int:
     parser.add_argument("--skip", type=float, default=3.0, help="leading seconds left out of every mean")
     parser.add_argument("--pause", type=float, default=3.0, help="idle seconds between workloads")
     parser.add_argument("--sample-every", type=float, default=0.2)
-    parser.add_argument("--workloads", default=",".join(WORKLOADS))
+    parser.add_argument("--workloads", default="grouped,single,hipblaslt")
     parser.add_argument("--kernel-config", default=None, metavar="BM,BN,BK,WARPS,STAGES,GROUP_M,MULT")
     args = parser.parse_args(argv)
     workloads = [w for w in args.workloads.split(",") if w]
@@ -128,6 +131,15 @@ def main(argv=None) -> int:
     assert flops == 2 * EXPERTS * GROUPED_SHAPE[0] * GROUPED_SHAPE[1] * GROUPED_SHAPE[2]
 
     steps = {}
+    flops_of = {name: flops for name in WORKLOADS}
+    if "decode" in workloads:
+        dws = build_grouped_workspace([DECODE_SHAPE] * EXPERTS, dtype, seed=1234)
+        flops_of["decode"] = 2 * EXPERTS * DECODE_SHAPE[0] * DECODE_SHAPE[1] * DECODE_SHAPE[2]
+        if pinned is None:
+            launch_grouped(dws)
+            steps["decode"] = lambda: launch_grouped(dws)
+        else:
+            steps["decode"] = lambda: launch_grouped(dws, config=pinned, autotune=False)
     if "grouped" in workloads:
         ws = build_grouped_workspace([GROUPED_SHAPE] * EXPERTS, dtype, seed=1234)
         if pinned is None:
@@ -157,7 +169,7 @@ def main(argv=None) -> int:
         ms, t_skip, t_end = sustained(steps[name], args.seconds, args.skip)
         power, clock, count = sampler.between(t_skip, t_end)
         fmt = lambda v: "n/a" if v is None else f"{v:.0f}"  # noqa: E731
-        print(f"| {name} | {ms * 1e3:.1f} | {flops / (ms * 1e9):.1f} | {fmt(power)} | {fmt(clock)} | {count} |",
+        print(f"| {name} | {ms * 1e3:.1f} | {flops_of[name] / (ms * 1e9):.1f} | {fmt(power)} | {fmt(clock)} | {count} |",
               flush=True)
         time.sleep(args.pause)
     sampler.stop()
