@@ -6,10 +6,15 @@ launch rules.  Only tests/, ``__graft_entry__.smoke()`` and bench.py's ``cpu_bas
 import this module, and only as the checker; the product path never does.
 
 Functions and the reference code they restate:
-  * ``gemm`` / ``grouped_gemm``     kernels/grouped_gemm.py:399-482 and kernels/matmul.py:223-273
-                                    (fp32-exact products, fp32/fp64 accumulation, cast on store);
-                                    pinned by tests/test_oracle.py against the golden fixtures
-                                    (torch CPU float64), closed forms, brute force and numpy.
+  * ``gemm``                        kernels/matmul.py:223-273 (fp32-exact products, fp32/fp64
+                                    accumulation, cast on store); pinned by tests/test_oracle.py
+                                    against the golden fixtures (torch CPU float64), closed forms,
+                                    brute force and numpy.
+  * ``grouped_gemm`` / ``grouped_gemm_tables``  kernels/grouped_gemm.py:399-482 over the tables of
+                                    :530-544 (pointer tables, dims (m, n, k), strides (am, ak, bk,
+                                    bn, cm, cn)); pinned against the golden fixtures, a brute force
+                                    and numpy on heterogeneous and strided groups, and by planted
+                                    table mistakes (dims order, stride order) that must fail.
   * ``tables``                      kernels/grouped_gemm.py:530-544 (pointer order, dims (m, n, k),
                                     strides (am, ak, bk, bn, cm, cn)); pinned by brute force.
   * ``is_homogeneous``              kernels/grouped_gemm.py:550-552; pinned by reference tests'
@@ -32,6 +37,8 @@ Functions and the reference code they restate:
   * ``offsets_tile_bound``          the host's tile-count bound for that layout (each group adds at
                                     most one partial M tile); pinned by exhaustive small cases.
   * ``to_bf16_bits`` / ``to_f16_bits``  round-to-nearest-even casts; pinned against torch/numpy.
+  * ``c_decode``                    the C decoders behind every operand read; pinned over all
+                                    65536 bit patterns against numpy's float16 and the bf16 shift.
   * ``gemm_fast_bf16``              the same fp32 running sum as ``gemm(accum="f32")``, blocked and
                                     threaded (an extra CPU timing in bench.py); pinned bit for bit
                                     against a numpy float32 running sum with torch's cast, against
@@ -75,7 +82,19 @@ def lib() -> ctypes.CDLL:
     handle.oracle_float_to_f16.restype = ctypes.c_uint16
     handle.oracle_tf32_round.argtypes = [ctypes.c_float]
     handle.oracle_tf32_round.restype = ctypes.c_float
+    handle.oracle_f16_to_float.argtypes = [ctypes.c_uint16]
+    handle.oracle_f16_to_float.restype = ctypes.c_float
+    handle.oracle_bf16_to_float.argtypes = [ctypes.c_uint16]
+    handle.oracle_bf16_to_float.restype = ctypes.c_float
     return handle
+
+
+def c_decode(bits: np.ndarray, dtype: str) -> np.ndarray:
+    """The C library's own 16-bit decoders (the ones oracle_gemm reads operands with)."""
+    handle = lib()
+    fn = handle.oracle_bf16_to_float if dtype == "bf16" else handle.oracle_f16_to_float
+    flat = np.ascontiguousarray(bits, dtype=np.uint16).ravel()
+    return np.array([fn(int(v)) for v in flat], dtype=np.float32).reshape(np.shape(bits))
 
 
 # --------------------------------------------------------------------------------------------
@@ -151,11 +170,54 @@ def gemm(a: np.ndarray, b: np.ndarray, dtype: str, *, tf32: bool = False, accum:
     return (c, sums) if return_sums else c
 
 
-def grouped_gemm(a_list, b_list, dtype: str, **kwargs):
-    """Per-problem ``gemm`` over a group (the reference's grouped kernel semantics)."""
+def grouped_gemm_tables(a_list, b_list, c_list, dims, strides, dtype: str, *, tf32: bool = False,
+                        accum: str = "f64") -> None:
+    """The reference's table form (kernels/grouped_gemm.py:530-544, read at :427-449): host pointer
+    tables over the arrays' first elements, ``dims`` int32 [G,3] = (m, n, k) and ``strides`` int64
+    [G,6] = (am, ak, bk, bn, cm, cn) in elements.  C_e is written through ``c_list[e]``'s memory as
+    the tables describe it; the arrays are not checked against the tables (as on the device)."""
+    groups = len(a_list)
+    if not groups or len(b_list) != groups or len(c_list) != groups:
+        raise ValueError("grouped GEMM requires matching, non-empty operand lists")
+    dims = np.ascontiguousarray(dims, dtype=np.int32)
+    strides = np.ascontiguousarray(strides, dtype=np.int64)
+    if dims.shape != (groups, 3) or strides.shape != (groups, 6):
+        raise ValueError("dims must be [G,3] and strides [G,6]")
+    table = ctypes.c_void_p * groups
+    a_ptrs = table(*(int(x.ctypes.data) for x in a_list))
+    b_ptrs = table(*(int(x.ctypes.data) for x in b_list))
+    c_ptrs = table(*(int(x.ctypes.data) for x in c_list))
+    rc = lib().oracle_grouped_gemm(groups, ctypes.addressof(a_ptrs), ctypes.addressof(b_ptrs),
+                                   ctypes.addressof(c_ptrs), dims.ctypes.data, strides.ctypes.data,
+                                   _DTYPES[dtype], int(tf32), ACCUM_F32 if accum == "f32" else ACCUM_F64)
+    if rc:
+        raise ValueError("oracle_grouped_gemm rejected its tables")
+
+
+def grouped_gemm(a_list, b_list, dtype: str, *, tf32: bool = False, accum: str = "f64"):
+    """C_e = A_e @ B_e for every problem, through the table form: dims and strides are taken from
+    the operand views exactly as the reference's builder takes them from its tensors
+    (kernels/grouped_gemm.py:536-544), so strided views keep their strides.  Returns the C list
+    (row-major, operand encoding)."""
     if not a_list or len(a_list) != len(b_list):
         raise ValueError("grouped GEMM requires matching, non-empty operand lists")
-    return [gemm(a, b, dtype, **kwargs) for a, b in zip(a_list, b_list)]
+    store = np.float32 if dtype == "fp32" else np.uint16
+    es = _element_size(dtype)
+    c_list, dims, strides = [], [], []
+    for a, b in zip(a_list, b_list):
+        a, b = np.asarray(a), np.asarray(b)
+        if a.dtype != store or b.dtype != store:
+            raise TypeError(f"{dtype} operands must be numpy {np.dtype(store).name} arrays")
+        (m, k), (kb, n) = a.shape, b.shape
+        if k != kb:
+            raise ValueError("inner dimensions differ")
+        c = np.zeros((m, n), dtype=store)
+        c_list.append(c)
+        dims.append((m, n, k))
+        strides.append((a.strides[0] // es, a.strides[1] // es, b.strides[0] // es, b.strides[1] // es,
+                        c.strides[0] // es, c.strides[1] // es))
+    grouped_gemm_tables(a_list, b_list, c_list, dims, strides, dtype, tf32=tf32, accum=accum)
+    return c_list
 
 
 def w13_reference(a: np.ndarray, b: np.ndarray, dtype: str, **kwargs) -> np.ndarray:

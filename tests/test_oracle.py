@@ -5,8 +5,11 @@ Each oracle function is checked against something it did not produce:
   * closed forms (A = 1, B = e + 1 => C = k (e + 1), the reference's known-answer test,
     tests/test_gpu.py:127-154) and a pure-Python brute force on tiny shapes;
   * numpy float64 matmul for strided views, torch / numpy casts for the rounding functions;
-  * planted mistakes (a transposed operand, a dropped K term, a shifted column): each must fail the
-    same comparison that the oracle passes, so the comparison has teeth.
+  * planted mistakes (a transposed operand, a dropped K term, a shifted column, dims in (m, k, n)
+    order, swapped strides, pointer tables out of step): each must fail the same comparison that
+    the oracle passes, so the comparison has teeth.
+A last test checks that every public oracle function and every symbol of liboracle.so is called
+here.
 """
 
 from __future__ import annotations
@@ -205,6 +208,22 @@ def test_tables_order_and_dispatch_rules():
     assert oracle.grid_size([(4096, 8, 4096)] * 4, 128, 128, 120, 2) == 240
 
 
+@pytest.mark.parametrize("m_tiles,n_tiles,group_m", [(1, 1, 8), (5, 3, 2), (9, 4, 4), (16, 7, 8), (3, 5, 1)])
+def test_group_m_tile_walks_bands_column_major(m_tiles, n_tiles, group_m):
+    # The traversal as nested loops: bands of group_m M tiles (the last one shorter); inside a
+    # band, N tiles in order and, for each, the band's M tiles in order.
+    expected = []
+    for first in range(0, m_tiles, group_m):
+        band = range(first, min(first + group_m, m_tiles))
+        expected += [(tm, tn) for tn in range(n_tiles) for tm in band]
+    got = [oracle.group_m_tile(t, m_tiles, n_tiles, group_m) for t in range(m_tiles * n_tiles)]
+    assert got == expected
+    if group_m > 1 and m_tiles > 1 and n_tiles > 1:  # a planted row-major band order differs
+        row_major = [(tm, tn) for first in range(0, m_tiles, group_m)
+                     for tm in range(first, min(first + group_m, m_tiles)) for tn in range(n_tiles)]
+        assert got != row_major
+
+
 @pytest.mark.parametrize("group_m", [1, 4, 8])
 @pytest.mark.parametrize("grid", [1, 7, 64])
 def test_tile_order_visits_every_tile_once(group_m, grid):
@@ -215,6 +234,165 @@ def test_tile_order_visits_every_tile_once(group_m, grid):
                 for tm in range(math.ceil(m / 64)) for tn in range(math.ceil(n / 64))}
     assert len(flat) == len(expected) == oracle.tile_count(shapes, 64, 64)
     assert set(flat) == expected
+
+
+# --------------------------------------------------------------------------------------------
+# Grouped table form: pointer tables, dims (m, n, k), strides (am, ak, bk, bn, cm, cn)
+# (reference kernels/grouped_gemm.py:427-449 reads them, :530-544 builds them)
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
+def test_grouped_gemm_heterogeneous_group_matches_golden(dtype):
+    names = [n for n in map(str, GOLDEN["case_names"]) if n.startswith(dtype + "_")]
+    assert len(names) >= 3
+    a_list = [GOLDEN[f"{n}_a"] for n in names]
+    b_list = [GOLDEN[f"{n}_b"] for n in names]
+    outs = oracle.grouped_gemm(a_list, b_list, dtype)
+    for name, out in zip(names, outs):
+        if dtype == "fp32":
+            np.testing.assert_allclose(out, GOLDEN[f"{name}_exact"].astype(np.float32), rtol=2e-7, atol=1e-12)
+        else:
+            np.testing.assert_array_equal(out, GOLDEN[f"{name}_out"])
+    # The grouped form agrees bit for bit with the single-problem form in both accumulation models.
+    for accum in ("f64", "f32"):
+        single = [oracle.gemm(a, b, dtype, accum=accum) for a, b in zip(a_list, b_list)]
+        for got, want in zip(oracle.grouped_gemm(a_list, b_list, dtype, accum=accum), single):
+            np.testing.assert_array_equal(got, want)
+
+
+_PAD = 4096  # every operand lives inside a zero-padded buffer, so planted table mistakes stay in bounds
+
+
+def _strided_group(dtype):
+    """Three heterogeneous problems, each with a different stride pattern, as (buffers, tables,
+    expected C).  Operand values are small integers, so every sum is exact before its one rounding."""
+    rng = np.random.default_rng(31)
+    store = np.float32 if dtype == "fp32" else np.uint16
+    encode = {"bf16": oracle.to_bf16_bits, "fp16": oracle.to_f16_bits,
+              "fp32": lambda v: np.asarray(v, np.float32)}[dtype]
+    problems = [(5, 7, 3), (17, 13, 31), (9, 20, 6)]  # (m, k, n): n != k everywhere
+    a_bufs, b_bufs, c_bufs, dims, strides, expect = [], [], [], [], [], []
+    for p, (m, k, n) in enumerate(problems):
+        av = rng.integers(-4, 5, (m, k)).astype(np.float32)
+        bv = rng.integers(-4, 5, (k, n)).astype(np.float32)
+        abuf = np.zeros(_PAD, store)
+        bbuf = np.zeros(_PAD, store)
+        if p == 0:    # A with a non-unit inner stride, B column-major, C column-major
+            am, ak, bk, bn, cm, cn = 2 * k, 2, 1, k, 1, m
+        elif p == 1:  # contiguous A, B rows padded past n, C rows padded past n
+            am, ak, bk, bn, cm, cn = k, 1, n + 9, 1, n + 5, 1
+        else:         # A transposed (column-major), B with both strides non-unit, C row-major
+            am, ak, bk, bn, cm, cn = 1, m, 2 * n + 1, 2, n, 1
+        for i in range(m):
+            for l in range(k):
+                abuf[i * am + l * ak] = encode(np.array([av[i, l]], np.float32))[0]
+        for l in range(k):
+            for j in range(n):
+                bbuf[l * bk + j * bn] = encode(np.array([bv[l, j]], np.float32))[0]
+        a_bufs.append(abuf)
+        b_bufs.append(bbuf)
+        c_bufs.append(np.zeros(_PAD, store))
+        dims.append((m, n, k))
+        strides.append((am, ak, bk, bn, cm, cn))
+        exact = np.array(_brute(av.tolist(), bv.tolist()), dtype=np.float32)
+        expect.append(_values(encode(exact), dtype))  # one rounding, by the casts pinned above
+    return a_bufs, b_bufs, c_bufs, dims, strides, expect
+
+
+def _gather_c(cbuf, dims_e, strides_e, dtype):
+    m, n, _ = dims_e
+    cm, cn = strides_e[4], strides_e[5]
+    idx = np.arange(m)[:, None] * cm + np.arange(n)[None, :] * cn
+    return _values(cbuf[idx], dtype)
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
+def test_grouped_gemm_tables_strided_heterogeneous_matches_brute_force(dtype):
+    a_bufs, b_bufs, c_bufs, dims, strides, expect = _strided_group(dtype)
+    oracle.grouped_gemm_tables(a_bufs, b_bufs, c_bufs, dims, strides, dtype)
+    for e in range(3):
+        np.testing.assert_array_equal(_gather_c(c_bufs[e], dims[e], strides[e], dtype), expect[e])
+        # Nothing outside the strided C footprint is written.
+        m, n, _ = dims[e]
+        cm, cn = strides[e][4], strides[e][5]
+        mask = np.ones(_PAD, bool)
+        mask[(np.arange(m)[:, None] * cm + np.arange(n)[None, :] * cn).ravel()] = False
+        assert not np.any(c_bufs[e][mask])
+
+
+@pytest.mark.parametrize("mistake", ["dims_m_k_n", "dims_n_m_k", "strides_ak_am", "strides_bn_bk",
+                                     "b_table_rotated"])
+def test_grouped_gemm_tables_planted_mistakes_fail(mistake):
+    dtype = "bf16"
+    a_bufs, b_bufs, c_bufs, dims, strides, expect = _strided_group(dtype)
+    dims_bad = [list(d) for d in dims]
+    strides_bad = [list(s) for s in strides]
+    b_bad = list(b_bufs)
+    if mistake == "dims_m_k_n":        # the reference's shape order (m, k, n) instead of (m, n, k)
+        dims_bad = [[m, k, n] for m, n, k in dims]
+    elif mistake == "dims_n_m_k":
+        dims_bad = [[n, m, k] for m, n, k in dims]
+    elif mistake == "strides_ak_am":   # A's two strides swapped
+        strides_bad = [[s[1], s[0], *s[2:]] for s in strides]
+    elif mistake == "strides_bn_bk":   # B's two strides swapped
+        strides_bad = [[s[0], s[1], s[3], s[2], s[4], s[5]] for s in strides]
+    else:                              # pointer tables out of step with each other
+        b_bad = b_bufs[1:] + b_bufs[:1]
+    oracle.grouped_gemm_tables(a_bufs, b_bad, c_bufs, dims_bad, strides_bad, dtype)
+    mismatched = 0
+    for e in range(3):
+        got = _gather_c(c_bufs[e], dims[e], strides[e], dtype)
+        mismatched += not np.array_equal(got, expect[e])
+    assert mismatched >= 1
+
+
+def test_grouped_gemm_tables_reject_bad_tables():
+    a_bufs, b_bufs, c_bufs, dims, strides, _ = _strided_group("fp16")
+    with pytest.raises(ValueError):
+        oracle.grouped_gemm_tables(a_bufs, b_bufs, c_bufs, [d[:2] for d in dims], strides, "fp16")
+    with pytest.raises(ValueError):
+        oracle.grouped_gemm_tables([], [], [], np.zeros((0, 3)), np.zeros((0, 6)), "fp16")
+    with pytest.raises(ValueError):
+        oracle.grouped_gemm(a_bufs[:1], [], "fp16")
+
+
+def test_c_decoders_exhaustive():
+    every = np.arange(0, 65536, dtype=np.uint32).astype(np.uint16)
+    got16 = oracle.c_decode(every, "fp16")
+    want16 = every.view(np.float16).astype(np.float32)
+    finite = np.isfinite(want16)
+    np.testing.assert_array_equal(got16[finite], want16[finite])
+    assert np.array_equal(np.isnan(got16), np.isnan(want16)) and np.array_equal(np.isinf(got16), np.isinf(want16))
+    gotb = oracle.c_decode(every, "bf16")
+    wantb = (every.astype(np.uint32) << 16).view(np.float32)
+    np.testing.assert_array_equal(gotb.view(np.uint32)[~np.isnan(wantb)], wantb.view(np.uint32)[~np.isnan(wantb)])
+    assert np.array_equal(np.isnan(gotb), np.isnan(wantb))
+
+
+def test_every_oracle_function_and_export_is_exercised_here():
+    """Every public function of oracle.py, and every symbol liboracle.so exports, is called by a
+    test in this file (so no part of the checker goes unpinned)."""
+    import inspect
+    import re
+    import subprocess
+
+    source = Path(__file__).read_text()
+    called = set(re.findall(r"oracle\.(\w+)\(", source))
+    public = {name for name, obj in vars(oracle).items()
+              if inspect.isfunction(obj) and obj.__module__ == oracle.__name__ and not name.startswith("_")}
+    helpers = {"lib"}  # the loader; every test goes through it
+    assert public - called - helpers == set()
+    exported = subprocess.run(["nm", "-D", "--defined-only", str(oracle.LIBRARY)], check=True,
+                              capture_output=True, text=True).stdout
+    symbols = {line.split()[-1] for line in exported.splitlines() if " T " in line}
+    bound = set(re.findall(r"handle\.(oracle_\w+)\.argtypes", Path(oracle.__file__).read_text()))
+    assert symbols and symbols == bound
+    # Each bound symbol is reached through a function this file calls.
+    reaches = {"oracle_gemm": "gemm", "oracle_grouped_gemm": "grouped_gemm_tables",
+               "oracle_gemm_rowmajor_fast": "gemm_fast_bf16", "oracle_float_to_bf16": "to_bf16_bits",
+               "oracle_float_to_f16": "to_f16_bits", "oracle_tf32_round": "tf32_round",
+               "oracle_f16_to_float": "c_decode", "oracle_bf16_to_float": "c_decode"}
+    assert set(reaches) == symbols
+    assert set(reaches.values()) <= called
 
 
 # --------------------------------------------------------------------------------------------
