@@ -155,7 +155,10 @@ int moegemm_matmul_splitk(const void* a, const void* b, void* c, int32_t m, int3
  *   - every call on one GPU shares that GPU's area: calls that overlap on one GPU (different
  *     streams or threads without ordering) race and may produce wrong results;
  *   - the first call on a GPU also launches one small kernel on `stream` that clears the counters
- *     (later launches leave them zero); the results equal moegemm_matmul_splitk's bit for bit.
+ *     (later launches leave them zero); the results equal moegemm_matmul_splitk's bit for bit;
+ *   - footprint: the array is part of the library's code object, so every process that loads the
+ *     library holds MOEGEMM_NOALLOC_SCRATCH_BYTES of device memory on each GPU the library is
+ *     loaded on, whether or not this entry point is ever called.
  */
 #define MOEGEMM_NOALLOC_SCRATCH_BYTES (64 * 1024 * 1024 + 256 * 1024)
 int moegemm_matmul_splitk_noalloc(const void* a, const void* b, void* c, int32_t m, int32_t n, int32_t k,

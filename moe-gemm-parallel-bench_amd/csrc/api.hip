@@ -90,12 +90,18 @@ int64_t splitk_bytes(int64_t tiles, int64_t splits, int64_t block_m, int64_t blo
   return kSplitCounterBytes + tiles * splits * block_m * block_n * 4;
 }
 
+// The K range of each split (whole K slices) and the split count that runs: trailing splits that
+// would be empty are dropped.  Shared by setup_splits and the no-allocation size check.
+void split_plan(int64_t k, int64_t splits, int64_t block_k, int64_t* chunk, int64_t* effective) {
+  *chunk = cdiv(cdiv(k, splits), block_k) * block_k;
+  *effective = cdiv(k, *chunk);
+}
+
 int setup_splits(KParams& p, int64_t tiles, int32_t k, int32_t splits, int32_t block_m, int32_t block_n,
                  int32_t block_k, void* workspace, int64_t workspace_bytes) {
   if (splits < 1 || splits > 64) return fail(MOEGEMM_ERR_INVALID, "splits must be in [1, 64] (got %d)", splits);
-  // Every split covers whole K slices; the effective count drops trailing empty splits.
-  const int64_t chunk = cdiv(cdiv(k, splits), block_k) * block_k;
-  const int64_t effective = cdiv(k, chunk);
+  int64_t chunk = 0, effective = 0;
+  split_plan(k, splits, block_k, &chunk, &effective);
   if (tiles * effective > INT32_MAX) return fail(MOEGEMM_ERR_INVALID, "split-K unit count exceeds int32");
   if (effective > 1) {
     if (tiles > kSplitMaxTiles)
@@ -371,14 +377,12 @@ int moegemm_matmul_splitk_noalloc(const void* a, const void* b, void* c, int32_t
                                   int64_t stride_cm, int64_t stride_cn, int32_t dtype, int32_t block_m,
                                   int32_t block_n, int32_t block_k, int32_t group_size_m, int32_t num_warps,
                                   int32_t num_stages, int32_t splits, int32_t grid_size, void* stream) {
-  void* area = nullptr;
-  int rc = device_scratch(stream, &area);
-  if (rc != MOEGEMM_OK) return rc;
-  // The split count that will run (trailing empty K ranges dropped) decides the bytes needed; reject
-  // a launch whose partials would not fit the static area before touching it.
+  // The split count that will run decides the bytes needed (split_plan, as setup_splits computes
+  // it); a launch whose partials would not fit the static area is rejected before anything runs.
+  // Other bad arguments are left to matmul_splitk_impl's checks.
   if (splits >= 1 && splits <= 64 && block_m > 0 && block_n > 0 && block_k > 0 && m > 0 && n > 0 && k > 0) {
-    const int64_t chunk = cdiv(cdiv(k, splits), block_k) * block_k;
-    const int64_t effective = cdiv(k, chunk);
+    int64_t chunk = 0, effective = 0;
+    split_plan(k, splits, block_k, &chunk, &effective);
     const int64_t need = splitk_bytes(cdiv(m, block_m) * cdiv(n, block_n), effective, block_m, block_n);
     if (effective > 1 && need > MOEGEMM_NOALLOC_SCRATCH_BYTES)
       return fail(MOEGEMM_ERR_INVALID,
@@ -386,6 +390,9 @@ int moegemm_matmul_splitk_noalloc(const void* a, const void* b, void* c, int32_t
                   "no-allocation entry point; use moegemm_matmul_splitk with a workspace",
                   (long long)need, (long long)MOEGEMM_NOALLOC_SCRATCH_BYTES);
   }
+  void* area = nullptr;
+  int rc = device_scratch(stream, &area);
+  if (rc != MOEGEMM_OK) return rc;
   return matmul_splitk_impl(a, b, c, m, n, k, stride_am, stride_ak, stride_bk, stride_bn, stride_cm, stride_cn, dtype,
                             block_m, block_n, block_k, group_size_m, num_warps, num_stages, splits, grid_size, area,
                             MOEGEMM_NOALLOC_SCRATCH_BYTES, stream);

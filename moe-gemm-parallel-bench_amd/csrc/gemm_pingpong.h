@@ -111,7 +111,8 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
     }
   }
 
-  // Cross-tile chaining on the static schedule of single and homogeneous launches.  A tile's last
+  // Cross-tile chaining on the static schedule of single and homogeneous launches, and of offsets
+  // launches whose groups fit one LDS prefix chunk (ragged groups, partial M tiles).  A tile's last
   // three memory phases would refill their buffers with zero slices past K; instead they copy the
   // next tile's slices 0..2 (each wave into its own slots, as always).  C then leaves through the
   // wave's slots of the last slice's buffer, in CHAIN_STORES counted stores

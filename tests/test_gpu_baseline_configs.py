@@ -7,7 +7,9 @@ on size:
     missing tile, duplicated tile or tail error anywhere in the group;
   * seeded random inputs checked on sampled experts against a float32 torch product on the GPU
     (normwise max|C - R| / max|R| <= 1e-2 for bf16, <= 2e-3 for fp16) and on sampled rows against
-    the CPU oracle (same bound).
+    the CPU oracle (same bound): once with the reference builder's normal * 0.1
+    (kernels/grouped_gemm.py:522-527), and for Mixtral and Qwen3 again with the distributions
+    their configurations state (N(0, 0.02) and U(-1, 1) * 0.05).
 """
 
 from __future__ import annotations
@@ -91,6 +93,43 @@ def test_full_size_random_sampled_against_references(case):
     a, b, c = workspace.a[-1], workspace.b[-1], workspace.c[-1]
     rows = slice(max(0, a.shape[0] - 4), a.shape[0])  # tail rows of the last expert, full N
     assert normwise(c[rows], oracle_product(a[rows], b)) <= NORMWISE[dtype]
+
+
+# The value distributions BASELINE configs[1] and configs[3] state for their inputs and weights:
+# Mixtral-8x7B N(0, 0.02), Qwen3-30B-A3B U(-1, 1) * 0.05.
+_STATED = {"mixtral": lambda t, g: t.normal_(0.0, 0.02, generator=g),
+           "qwen3": lambda t, g: t.uniform_(-1.0, 1.0, generator=g).mul_(0.05)}
+STATED_CASES = [c for c in ALL_CASES if c[0].split("_")[0] in _STATED]
+
+
+@pytest.mark.parametrize("case", STATED_CASES, ids=[c[0] for c in STATED_CASES])
+def test_full_size_stated_input_distribution(case):
+    """Every expert's A and B redrawn from the configuration's stated distribution, then the tuned
+    launch checked on sampled experts against a float32 torch product and on the last expert's
+    tail rows against the CPU oracle (normwise bound of the dtype)."""
+    from kernels.grouped_gemm import launch_grouped
+
+    name, projection, parallel, m, h, f, e, p, dtype = case
+    print(f"stated distribution full size {name}", flush=True)
+    workspace = _workspace(projection, parallel, m, h, f, e, p, dtype)
+    draw = _STATED[name.split("_")[0]]
+    generator = torch.Generator(device="cuda").manual_seed(4321)
+    for a, b, c in workspace.problem_tensors():
+        draw(a, generator)
+        draw(b, generator)
+        c.fill_(float("nan"))
+    launch_grouped(workspace)
+    for c in workspace.c:
+        c.fill_(float("nan"))
+    launch_grouped(workspace, config=workspace.config, autotune=False)
+    torch.cuda.synchronize()
+    for index in sorted({0, workspace.problem_count // 2, workspace.problem_count - 1}):
+        a, b, c = workspace.a[index], workspace.b[index], workspace.c[index]
+        assert torch.isfinite(c).all(), f"{name}: expert {index} left unwritten"
+        assert normwise(c, a.float() @ b.float()) <= NORMWISE[dtype], f"{name}: expert {index}"
+    a, b, c = workspace.a[-1], workspace.b[-1], workspace.c[-1]
+    rows = slice(max(0, a.shape[0] - 4), a.shape[0])
+    assert normwise(c[rows], oracle_product(a[rows], b)) <= NORMWISE[dtype], f"{name}: oracle tail rows"
 
 
 def test_heatmap_tail_shapes_against_oracle():

@@ -4,7 +4,7 @@
   and one torch.mm row per point, every HIP row gated against torch per problem before timing,
   the run passing the harness validator (FLOPs recomputed from M, K, N and num_gemms);
 * the MoE driver, hot with the expert-sorted layout and torch grouped_mm rows, and rotating-cold
-  with its ring tuner, on small EP/TP per-rank shapes;
+  with its ring tuner, on small EP/TP per-rank shapes and at DeepSeek-V3's full per-rank shapes;
 * the comparison runner against the per-expert hipBLASLt loop (NaN-poisoned, checked candidates,
   two reversed rounds), and its verdict on a contender that writes nothing;
 * the torch grouped_mm provider: admitted or not by its trace check, its results are right;
@@ -91,6 +91,34 @@ def test_moe_driver_rotating_cold_ring(tmp_path):
         assert row["status"] == "ok" and row["config_source"] == "cold_ring_autotune"
         assert row["workspace_count"] == "2" and int(row["autotune_candidates_tested"]) > 0
         assert int(row["repeat"]) % 2 == 0  # whole rings
+
+
+def test_moe_driver_rotating_cold_full_size_dsv3(tmp_path):
+    """DeepSeek-V3 at its real per-rank shapes (P = 8) in the rotating-cold regime with two
+    resident workspaces, M_e in {8, 512}: the ring admission, the cold-ring tuner and the gate on
+    every buffer, for W13 and W2, EP and TP (reference benchmark_moe.py:155-206)."""
+    from harness.cli import main
+    from utils.io import read_rows
+
+    results = tmp_path / "dsv3_cold"
+    print("driver moe cold DSV3 full size M=8,512 ring=2", flush=True)
+    assert main(["--experiment", "moe", "--dtype", "bf16", "--model-config", "model_configs/deepseek-v3.json",
+                 "--parallel-size", "8", "--moe-ms", "8,512", "--cache-mode", "cold", "--cold-buffers", "2",
+                 "--no-torch-baseline", "--warmup", "2", "--repeat", "6", "--target-timing-ms", "50",
+                 "--results-dir", str(results)]) == 0
+    shapes = {("w1", "EP"): (32, 7168, 4096), ("w1", "TP"): (256, 7168, 512),
+              ("w2", "EP"): (32, 2048, 7168), ("w2", "TP"): (256, 256, 7168)}  # (G, K, N) per rank
+    for projection in ("w1", "w2"):
+        rows = read_rows(results / f"moe_{projection}.csv")
+        assert len(rows) == 4, [(r["parallel_type"], r["M"], r["status"]) for r in rows]
+        assert {(r["parallel_type"], int(r["M"])) for r in rows} == {(p, m) for p in ("EP", "TP") for m in (8, 512)}
+        for row in rows:
+            label = f"{projection} {row['parallel_type']} M={row['M']}: {row['skip_reason'] or row['error']}"
+            assert row["status"] == "ok" and row["correct"] == "True", label
+            assert row["config_source"] == "cold_ring_autotune" and row["workspace_count"] == "2", label
+            assert int(row["repeat"]) % 2 == 0, label  # whole rings
+            got = (int(row["num_gemms"]), int(row["K"]), int(row["N"]))
+            assert got == shapes[projection, row["parallel_type"]], label
 
 
 def test_compare_runner_against_the_hipblaslt_loop(tmp_path):

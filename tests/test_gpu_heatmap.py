@@ -1,12 +1,15 @@
-"""GPU parity over the heatmap family of single grouped GEMMs (bf16, N(0,1)/sqrt(K)-style inputs).
+"""GPU parity over the heatmap family of single grouped GEMMs (bf16, seeded N(0,1)/sqrt(K) inputs).
 
 The grid extends the reference's single-GEMM heatmap (benchmark_shapes.py:321-335, G = 1) to
 G in {1, 8, 64, 256} groups of equal problems, with extents that are not tile multiples
-(2880 = 22.5 x 128, from gpt-oss-120b).  Every point is launched through ``launch_grouped`` with
-the heuristic config (G = 1 dispatches to the single GEMM, whose heuristic may split K), and checked
+(2880 = 22.5 x 128, from gpt-oss-120b): all 500 points, M_e in {8, 32, 128, 512, 2048} x N, K in
+{256, 1024, 2880, 4096, 7168} at every G, from 256 x [8,256]@[256,256] up to
+256 x [2048,7168]@[7168,7168].  Every point is launched through ``launch_grouped`` with the
+heuristic config (G = 1 dispatches to the single GEMM, whose heuristic may split K), and checked
 three ways, in the pattern of the reference's tests/test_gpu.py:127-154:
-  * seeded random inputs: the first and last problem against a float32 torch product on the GPU
-    (normwise max|C - R| / max|R| <= 1e-2), and tail rows of both against the CPU oracle;
+  * seeded random inputs drawn N(0,1)/sqrt(K), as the configuration states: the first and last
+    problem against a float32 torch product on the GPU (normwise max|C - R| / max|R| <= 1e-2),
+    and tail rows of both against the CPU oracle;
   * exact integers on every problem: A = 1, B_e = e % 31 + 1, so C_e = K (e % 31 + 1) exactly in
     the fp32 accumulator, rounded to bf16 the same way as the expected value - a wrong problem
     index, a skipped or duplicated tile, or a missed tail shows on whichever problem it hits;
@@ -24,8 +27,7 @@ pytestmark = pytest.mark.gpu
 
 EXTENTS = (256, 1024, 2880, 4096, 7168)
 SMALL_GROUPS = [(g, m, n, k) for g in (1, 8) for m in (8, 32, 128, 512, 2048) for n in EXTENTS for k in EXTENTS]
-LARGE_GROUPS = [(g, m, n, k) for g in (64, 256) for m in (8, 32, 512) for n in (1024, 2880, 4096)
-                for k in (1024, 2880, 7168)]
+LARGE_GROUPS = [(g, m, n, k) for g in (64, 256) for m in (8, 32, 128, 512, 2048) for n in EXTENTS for k in EXTENTS]
 
 
 @pytest.fixture(autouse=True)
@@ -39,7 +41,10 @@ def _check_point(g: int, m: int, n: int, k: int) -> None:
 
     print(f"heatmap G={g} M={m} N={n} K={k}", flush=True)
     workspace = build_grouped_workspace([(m, k, n)] * g, torch.bfloat16, seed=m * 7 + n * 3 + k + g)
-    for c in workspace.c:
+    generator = torch.Generator(device="cuda").manual_seed(m * 7 + n * 3 + k + g)
+    for a, b, c in workspace.problem_tensors():
+        a.normal_(generator=generator).div_(k ** 0.5)
+        b.normal_(generator=generator).div_(k ** 0.5)
         c.fill_(float("nan"))
     launch_grouped(workspace, autotune=False)
     torch.cuda.synchronize()

@@ -40,6 +40,10 @@ def _oracle(mat_a, mat_b, offs_list):
     return from_oracle(c, name)
 
 
+def _small_ints(shape, dtype=torch.bfloat16):
+    return torch.randint(-2, 3, shape, device="cuda").to(dtype)
+
+
 def _operands(rows, k, n, groups, dtype, *, integer=False):
     if integer:
         mat_a = torch.ones((rows, k), device="cuda", dtype=dtype)
@@ -227,16 +231,19 @@ def test_dsv3_lognormal_routing_exact_and_oracle(schedule, mean):
         tail = slice(max(r1 - 3, r1 - sizes[e]), r1)
         expected = from_oracle(oracle.gemm(to_oracle(mat_a[tail]), to_oracle(mat_b[e]), "bf16"), "bf16")
         assert normwise(out[tail].cpu(), expected) <= 1e-2, f"expert {e}"
-    mat_a.fill_(1)
-    for e in range(groups):
-        mat_b[e].fill_(e % 31 + 1)
+    # Exact check of every row: small random integers in A and in each expert's B, so every fp32
+    # sum is an exact integer (|sum| <= 4 K < 2^24) and the one rounding to bf16 is the reference's
+    # own.  An fp32 torch product of integer operands is exact too, whatever its summation order.
+    mat_a.copy_(_small_ints((rows, k)))
+    mat_b.copy_(_small_ints((groups, k, n)))
     out.fill_(float("nan"))
     grouped_mm(mat_a, mat_b, offs, out=out, tile_schedule=schedule)
     torch.cuda.synchronize()
     for e in range(groups):
         r0, r1 = (offs_list[e - 1] if e else 0), offs_list[e]
         if r1 > r0:
-            assert torch.equal(out[r0:r1], torch.full_like(out[r0:r1], float(k * (e % 31 + 1)))), f"expert {e}"
+            expected = (mat_a[r0:r1].float() @ mat_b[e].float()).to(torch.bfloat16)
+            assert torch.equal(out[r0:r1], expected), f"expert {e}"
 
 
 @pytest.mark.parametrize("schedule", ["static", "stealing"])
@@ -245,22 +252,23 @@ def test_chained_tiles_on_ragged_offsets_small_grids(k, schedule):
     """Offsets launches whose groups fit one prefix chunk run the chained schedule: every chained
     tile (two-stage tiles up to 64 rows, the ping-pong tile), at grids that give each workgroup many
     ragged tiles, empty groups included, rows past the last offset left untouched, static and
-    stealing.  A is small integers and each group's B is a constant, so every row's exact value is
-    known: k * sum(A row) * b_e, here with A = 1 and b_e = e % 7 + 1."""
+    stealing.  A and every group's B hold small random integers, so each output is an exact integer
+    sum rounded once to bf16: a stale or wrong K slice, N tile or M tile, even from the same group,
+    changes some row, and every row is compared bit for bit with a float64 product per group."""
     from kernels import _native
 
     sizes = [70, 0, 3, 130, 257, 0, 1, 64, 200, 9]
     ends = list(np.cumsum(sizes))
     groups, rows, n = len(sizes), int(ends[-1]), 392
     spare = 5  # rows past the last offset: never written
-    mat_a = torch.ones((rows + spare, k), device="cuda", dtype=torch.bfloat16)
-    mat_b = torch.stack([torch.full((k, n), float(e % 7 + 1), device="cuda", dtype=torch.bfloat16)
-                         for e in range(groups)])
+    mat_a = _small_ints((rows + spare, k))
+    mat_b = _small_ints((groups, k, n))
     offs = torch.tensor(ends, device="cuda", dtype=torch.int32)
+    a64, b64 = mat_a.double().cpu(), mat_b.double().cpu()
     expected = torch.full((rows + spare, n), float("nan"), dtype=torch.float64)
     prev = 0
     for e, end in enumerate(ends):
-        expected[prev:end] = float(k * (e % 7 + 1))
+        expected[prev:end] = a64[prev:end] @ b64[e]
         prev = end
     expected = expected.to(torch.bfloat16)
     chained = [t for t in _native.compiled_kernels(_native.DTYPE_BF16)
@@ -285,5 +293,6 @@ def test_chained_tiles_on_ragged_offsets_small_grids(k, schedule):
                 assert not queue.any(), f"queue not re-armed: {queue.tolist()}"
             label = f"{schedule} k {k} tile {(bm, bn, bk, warps, stages)} grid {grid}"
             got = out.cpu()
-            assert torch.equal(got[:rows], expected[:rows]), label
+            bad = (got[:rows] != expected[:rows]).any(dim=1).nonzero().flatten().tolist()
+            assert not bad, f"{label}: rows {bad[:8]} differ"
             assert torch.isnan(got[rows:]).all(), label
