@@ -8,6 +8,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -73,6 +74,11 @@ int check_common(int dtype, int input_precision, int group_size_m, const KernelE
 
 int launch(const KernelEntry* e, KParams& p, int grid, bool vector_layout, void* stream) {
   LaunchFn fn = (vector_layout && e->launch_fast) ? e->launch_fast : e->launch_general;
+  if (p.splits > 1) {  // split-K units: the fast path's split kernel (the callers checked the layout)
+    if (!vector_layout || !e->launch_fast_split)
+      return fail(MOEGEMM_ERR_INVALID, "split-K needs fp16/bf16 operands in the vector layout");
+    fn = e->launch_fast_split;
+  }
   hipError_t err = fn(p, grid, reinterpret_cast<hipStream_t>(stream));
   if (err != hipSuccess) return fail(MOEGEMM_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
   return MOEGEMM_OK;
@@ -88,6 +94,16 @@ constexpr int64_t kSplitMaxTiles = kSplitCounterBytes / 4;
 
 int64_t splitk_bytes(int64_t tiles, int64_t splits, int64_t block_m, int64_t block_n) {
   return kSplitCounterBytes + tiles * splits * block_m * block_n * 4;
+}
+
+// Polls a split-K unit makes of its tile's counter while it waits for the tile's other units (see
+// FastTile::split_store).  MOEGEMM_SPLIT_POLLS overrides the default of 16 (0 = never wait); tests
+// set it to force the path where units stop waiting.
+int32_t split_polls() {
+  const char* env = std::getenv("MOEGEMM_SPLIT_POLLS");
+  if (!env || !*env) return 16;
+  const long v = std::strtol(env, nullptr, 10);
+  return v < 0 ? 0 : v > 4096 ? 4096 : (int32_t)v;
 }
 
 // The K range of each split (whole K slices) and the split count that runs: trailing splits that
@@ -118,6 +134,7 @@ int setup_splits(KParams& p, int64_t tiles, int32_t k, int32_t splits, int32_t b
   }
   p.splits = (int32_t)effective;
   p.k_chunk = (int32_t)chunk;
+  p.split_polls = split_polls();
   p.total_tiles = (int32_t)tiles;
   return MOEGEMM_OK;
 }

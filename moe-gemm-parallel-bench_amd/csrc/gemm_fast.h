@@ -340,40 +340,129 @@ struct FastTile {
 
   // Split-K reduction through LDS: after the K loop the DMA ring is free, and each wave takes
   // RED_SLOTS 1 KiB slots of it.  The wave's share of one partial is RED_CH 1 KiB chunks (each lane
-  // fetches the 16 bytes of its own accumulator chunk, landing at slot + 16 * lane).  A round copies
-  // RED_R splits x RED_CB chunks (at most RED_CAP copies in flight per wave), waits once, and adds
-  // them from LDS, so many partials share one memory round trip.  The sum of every element runs in
-  // split order.  KEEP_OWN tiles add their own partial from the accumulators; larger tiles read it
-  // back like the others, so that the accumulators are dead and the registers free.
+  // fetches the 16 bytes of its own accumulator chunk, landing at slot + 16 * lane).  A chunk range
+  // is reduced in rounds: each round copies as many (split, chunk) pairs as fit RED_CAP slots per
+  // wave, waits once, and adds them from LDS, so many partials share one memory round trip.  The sum
+  // of every element runs in split order, whichever unit reduces it.  KEEP_OWN tiles add their own
+  // partial from the accumulators; larger tiles read it back like the others, so that the
+  // accumulators are dead and the registers free.
   static constexpr int RED_CH = FM * FN * (ACC / 4);
   static constexpr int RED_SLOTS = (STAGES * STAGE_BYTES / NW) / 1024;
   static constexpr int RED_CAP = RED_SLOTS < 48 ? RED_SLOTS : 48;
-  static constexpr int RED_CB = RED_CH < RED_CAP ? RED_CH : RED_CAP;
-  static constexpr int RED_R = RED_CAP / RED_CB;
   static constexpr bool KEEP_OWN = 2 * FM * FN * ACC <= 160;
-  static_assert(RED_CAP >= 1 && RED_R >= 1, "at least one 1 KiB slot per wave for the split-K reduction");
+  static_assert(RED_CAP >= 1, "at least one 1 KiB slot per wave for the split-K reduction");
+  // Shared reductions (split_store): at most this many splits, and only when one unit would read at
+  // least this many chunks per wave of the other units' partials; below that the extra round trips
+  // of waiting cost more than the reads they spread.
+  static constexpr int kSharedMaxSplits = 16;
+  static constexpr int kSharedMinChunks = 48;
 
-  // Byte offset, inside one partial tile, of this lane's 16-byte accumulator chunk (fm, fn, q).
-  // Partials are private scratch, laid out in accumulator order [wave][chunk][lane][4 floats]: each
-  // wave's store or load of one chunk is one contiguous 1 KiB access (a row-major tile would give
-  // every instruction 16 bytes in each of 32 rows).  Every unit of a tile runs the same tile, so
-  // chunk (wave, c) holds the same output elements in every split's partial.
-  __device__ static __forceinline__ int chunk_offset(int fm, int fn, int q, int wave) {
+  // Byte offset, inside one partial tile, of this lane's 16-byte accumulator chunk c (= (fm * FN +
+  // fn) * ACC / 4 + q).  Partials are private scratch, laid out in accumulator order
+  // [wave][chunk][lane][4 floats]: each wave's store or load of one chunk is one contiguous 1 KiB
+  // access (a row-major tile would give every instruction 16 bytes in each of 32 rows).  Every unit
+  // of a tile runs the same tile, so chunk (wave, c) holds the same output elements in every split's
+  // partial.
+  __device__ static __forceinline__ int chunk_offset(int c, int wave) {
     const int lane = threadIdx.x & 63;
-    const int c = (fm * FN + fn) * (ACC / 4) + q;
     return ((wave * RED_CH + c) * 64 + lane) * 16;
   }
 
-  __device__ static __forceinline__ void split_store(const acc_t (&acc)[FM][FN], const ProblemDesc& pd, int m0,
-                                                     int n0, int wave_m, int wave_n, char* smem) {
-    __shared__ int s_last;
+  // Sums chunks [lo, hi) of every split's partial (split order) and stores them to C.
+  __device__ static __forceinline__ void reduce_chunks(const acc_t (&acc)[FM][FN], const ProblemDesc& pd, int m0,
+                                                       int n0, int wave_m, int wave_n, char* smem, int lo, int hi) {
+    constexpr uint32_t kSlotBytes = BM * BN * 4;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    // Partial slot of split sp: [tiles][splits][BM * BN] floats.
-    constexpr uint32_t kSlotBytes = BM * BN * 4;
-    auto slot_base = [&](int sp) { return pd.partials + ((int64_t)pd.tile * pd.splits + sp) * (BM * BN); };
-    const auto mine = __builtin_amdgcn_make_buffer_rsrc(slot_base(pd.split), (short)0, (int)kSlotBytes,
-                                                        (int)kBufferFlags);
+    const int splits = pd.splits;
+    char* region = smem + wave * RED_SLOTS * 1024;
+    const uint32_t region_lds = lds_address(region);
+    acc_t tot[FM][FN];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int i = 0; i < ACC; ++i) tot[fm][fn][i] = 0.0f;
+    // Rounds of `per` chunks x `ways` splits (at most RED_CAP copies in flight per wave).
+    const int per = min(hi - lo, RED_CAP), ways = max(1, RED_CAP / per);
+    for (int c0 = lo; c0 < hi; c0 += per) {
+      const int cn = min(per, hi - c0);
+      for (int g0 = 0; g0 < splits; g0 += ways) {
+        const int count = min(ways, splits - g0);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the previous round's LDS reads are done
+        for (int r = 0; r < count; ++r) {
+          if (KEEP_OWN && g0 + r == pd.split) continue;
+          const u32x4_t rs = make_rsrc(pd.partials + ((int64_t)pd.tile * splits + g0 + r) * (BM * BN), kSlotBytes);
+          for (int i = 0; i < cn; ++i)
+            dma_copy16_coherent(rs, (uint32_t)chunk_offset(c0 + i, wave), region_lds + (uint32_t)((r * per + i) * 1024));
+        }
+        wait_vmcnt<0>();
+        compiler_fence();
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+            for (int q = 0; q < ACC / 4; ++q) {
+              const int c = (fm * FN + fn) * (ACC / 4) + q;
+              if (c < c0 || c >= c0 + cn) continue;
+              for (int r = 0; r < count; ++r) {
+                f32x4_t v;
+                if (KEEP_OWN && g0 + r == pd.split)
+                  v = f32x4_t{acc[fm][fn][q * 4 + 0], acc[fm][fn][q * 4 + 1], acc[fm][fn][q * 4 + 2],
+                              acc[fm][fn][q * 4 + 3]};
+                else
+                  v = *reinterpret_cast<const f32x4_t*>(region + (r * per + (c - c0)) * 1024 + lane * 16);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) tot[fm][fn][q * 4 + i] += v[i];
+              }
+            }
+        compiler_fence();
+      }
+    }
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      const int gm = m0 + wave_m * WTM + fm * MI + (lane % MI);
+      char* crow = pd.c + (int64_t)gm * pd.scm * 2;
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int q = 0; q < ACC / 4; ++q) {
+          const int c = (fm * FN + fn) * (ACC / 4) + q;
+          if (c < lo || c >= hi) continue;
+          const int cl = wave_n * WTN + fn * MI + ((MI == 32) ? (q * 8 + (lane >> 5) * 4) : ((lane >> 4) * 4));
+          if (gm >= pd.m || n0 + cl >= pd.n) continue;
+          const f32x4_t v = {tot[fm][fn][q * 4 + 0], tot[fm][fn][q * 4 + 1], tot[fm][fn][q * 4 + 2],
+                             tot[fm][fn][q * 4 + 3]};
+          store4<E>(crow + (int64_t)(n0 + cl) * 2, v);
+        }
+    }
+  }
+
+  // Split-K epilogue of one unit.  The unit stores its fp32 partial (device-coherent sc1 stores),
+  // waits for them, and arrives at the tile's counter, one int32 per tile.  Then one of two
+  // protocols, the same for every unit of the tile:
+  //  * single (few chunks to read, or the units of the launch share workgroups, pd.split_wait 0):
+  //    the last unit to arrive reduces the whole tile and re-arms the counter to zero;
+  //  * shared: the tile's chunks form `splits` slices (slice s = chunks [s RED_CH / S,
+  //    (s + 1) RED_CH / S)), and unit s reduces slice s once every unit has arrived.  Counter
+  //    fields: arrivals (bits 0-7), a mask of units that stopped waiting (bits 8-23) and departures
+  //    (bits 24-31).  A unit that is not the last to arrive polls the counter up to pd.split_wait
+  //    times, each after a sleep of about 1000 cycles (the host's default of 16 polls waits some
+  //    20-30 us); if the others have still not arrived, it sets its bit with a compare-and-swap that
+  //    succeeds only while arrivals are short, and leaves its slice.  The last unit to arrive reads
+  //    the mask in the value its arrival returned (every bit was set before that arrival) and
+  //    reduces those slices as well as its own, so every slice is reduced exactly once.  Each unit
+  //    then departs, and the unit whose departure completes the count re-arms the counter.
+  // Launches and graph replays need no memset.
+  __device__ static __forceinline__ void split_store(const acc_t (&acc)[FM][FN], const ProblemDesc& pd, int m0,
+                                                     int n0, int wave_m, int wave_n, char* smem) {
+    __shared__ uint32_t s_work;  // bit s: reduce slice s; bit 31: reduce the whole tile
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int splits = pd.splits;
+    const auto mine = __builtin_amdgcn_make_buffer_rsrc(pd.partials + ((int64_t)pd.tile * splits + pd.split) * (BM * BN),
+                                                        (short)0, (int)(BM * BN * 4), (int)kBufferFlags);
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
@@ -382,7 +471,7 @@ struct FastTile {
         for (int q = 0; q < ACC / 4; ++q) {
           const f32x4_t v = {acc[fm][fn][q * 4 + 0], acc[fm][fn][q * 4 + 1], acc[fm][fn][q * 4 + 2],
                              acc[fm][fn][q * 4 + 3]};
-          __builtin_amdgcn_raw_buffer_store_b128(v, mine, chunk_offset(fm, fn, q, wave), 0,
+          __builtin_amdgcn_raw_buffer_store_b128(v, mine, chunk_offset((fm * FN + fn) * (ACC / 4) + q, wave), 0,
                                                  kDeviceCoherent);
         }
     // The partials are device-coherent (sc1) stores, the encoding of relaxed agent-scope atomic
@@ -391,81 +480,60 @@ struct FastTile {
     // before the counter moves.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    const bool shared = pd.split_wait > 0 && splits <= kSharedMaxSplits && RED_CH * (splits - 1) >= kSharedMinChunks;
+    int32_t* word = pd.counters + pd.tile;
     if (threadIdx.x == 0) {
-      const int last = atomicAdd(pd.counters + pd.tile, 1) == pd.splits - 1;
-      if (last) atomicExch(pd.counters + pd.tile, 0);
-      s_last = last;
+      const uint32_t old = (uint32_t)atomicAdd(word, 1);
+      const bool last = (int)(old & 0xffu) == splits - 1;
+      uint32_t work = 0;
+      if (!shared) {
+        if (last) {
+          atomicExch(word, 0);
+          work = 1u << 31;
+        }
+      } else if (last) {
+        work = ((old >> 8) & 0xffffu) | (1u << pd.split);
+      } else {
+        work = 1u << pd.split;
+        uint32_t w = 0;
+        for (int poll = 0;; ++poll) {
+          __builtin_amdgcn_s_sleep(16);
+          w = (uint32_t)__hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if ((int)(w & 0xffu) >= splits || poll + 1 >= pd.split_wait) break;
+        }
+        // Stop waiting: set this unit's bit while arrivals are still short.  Each failed
+        // compare-and-swap means another arrival or another unit's bit changed the word, at most
+        // 2 x splits times.
+        while ((int)(w & 0xffu) < splits) {
+          const uint32_t seen = (uint32_t)atomicCAS(word, (int)w, (int)(w | (1u << (8 + pd.split))));
+          if (seen == w) {
+            work = 0;
+            break;
+          }
+          w = seen;
+        }
+      }
+      s_work = work;
     }
     __syncthreads();
-    if (!s_last) return;
-    // The last unit reads the other partials with device-coherent (sc1) loads, issued after the
-    // counter showed all other units' stores complete: no L2 invalidation (acquire fence) is
-    // needed.  Every element sums the partials in split order, so the result is the same whichever
-    // unit is last.
-    acc_t tot[FM][FN];
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-      for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-        for (int i = 0; i < ACC; ++i) tot[fm][fn][i] = 0.0f;
-    auto add_chunk = [&](int fm, int fn, int q, const f32x4_t& v) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) tot[fm][fn][q * 4 + i] += v[i];
-    };
-    char* region = smem + wave * RED_SLOTS * 1024;
-    const uint32_t region_lds = lds_address(region);
-#pragma unroll
-    for (int cb = 0; cb < RED_CH; cb += RED_CB) {
-      for (int g0 = 0; g0 < pd.splits; g0 += RED_R) {
-        const int count = min(RED_R, pd.splits - g0);
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the previous round's LDS reads are done
-        for (int r = 0; r < count; ++r) {
-          const int sp = g0 + r;
-          if (KEEP_OWN && sp == pd.split) continue;
-          const u32x4_t rs = make_rsrc(slot_base(sp), kSlotBytes);
-#pragma unroll
-          for (int i = 0; i < RED_CB; ++i)
-            if (cb + i < RED_CH)
-              dma_copy16_coherent(rs, (uint32_t)(((wave * RED_CH + cb + i) * 64 + lane) * 16),
-                                  region_lds + (uint32_t)((r * RED_CB + i) * 1024));
-        }
-        wait_vmcnt<0>();
-        compiler_fence();
-        for (int r = 0; r < count; ++r) {
-          const bool own = KEEP_OWN && g0 + r == pd.split;
-#pragma unroll
-          for (int i = 0; i < RED_CB; ++i) {
-            const int c = cb + i;
-            if (c >= RED_CH) continue;
-            const int fm = c / (FN * (ACC / 4)), fn = (c / (ACC / 4)) % FN, q = c % (ACC / 4);
-            if (own)
-              add_chunk(fm, fn, q, f32x4_t{acc[fm][fn][q * 4 + 0], acc[fm][fn][q * 4 + 1], acc[fm][fn][q * 4 + 2],
-                                           acc[fm][fn][q * 4 + 3]});
-            else
-              add_chunk(fm, fn, q, *reinterpret_cast<const f32x4_t*>(region + (r * RED_CB + i) * 1024 + lane * 16));
-          }
-        }
-        compiler_fence();
+    // Every partial of the tile has completed once this unit has work: its sc1 loads see them (no
+    // L2 invalidation, acquire fence, is needed).
+    const uint32_t work = (uint32_t)uniform((int32_t)s_work);
+    if (work >> 31) {
+      reduce_chunks(acc, pd, m0, n0, wave_m, wave_n, smem, 0, RED_CH);
+    } else if (work) {
+      for (int sl = 0; sl < splits; ++sl) {
+        const int lo = sl * RED_CH / splits, hi = (sl + 1) * RED_CH / splits;
+        if (((work >> sl) & 1u) && lo < hi) reduce_chunks(acc, pd, m0, n0, wave_m, wave_n, smem, lo, hi);
       }
     }
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm) {
-      const int rl = wave_m * WTM + fm * MI + (lane % MI);
-      const int gm = m0 + rl;
-      if (gm >= pd.m) continue;
-      char* crow = pd.c + (int64_t)gm * pd.scm * 2;
-#pragma unroll
-      for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-        for (int q = 0; q < ACC / 4; ++q) {
-          const int cl = wave_n * WTN + fn * MI + ((MI == 32) ? (q * 8 + (lane >> 5) * 4) : ((lane >> 4) * 4));
-          if (n0 + cl >= pd.n) continue;
-          const f32x4_t v = {tot[fm][fn][q * 4 + 0], tot[fm][fn][q * 4 + 1], tot[fm][fn][q * 4 + 2],
-                             tot[fm][fn][q * 4 + 3]};
-          store4<E>(crow + (int64_t)(n0 + cl) * 2, v);
-        }
-    }
+    if (shared && threadIdx.x == 0 && (int)(((uint32_t)atomicAdd(word, 1 << 24) >> 24) & 0xffu) == splits - 1)
+      atomicExch(word, 0);
+    // Each wave reduced through a contiguous LDS region of its own, which is not the slot ownership
+    // of the copies: the workgroup's next unit must not issue its first copies (into other waves'
+    // regions) until every wave has finished reading.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __syncthreads();
   }
 
   // LDS byte offset (from the tile's LDS base) of the s-th 1 KiB slot this wave fills by DMA:
@@ -526,12 +594,13 @@ struct FastTile {
     }
   }
 
-  // Stores the tile (C, the SwiGLU output, or split-K partials).  The wave's copies must have
-  // landed (the staged epilogue reuses its LDS slots).
+  // Stores the tile (C, the SwiGLU output, or, in the split-K kernel, split-K partials).  The
+  // wave's copies must have landed (the staged epilogue reuses its LDS slots).
+  template <bool SPLIT = false>
   __device__ static __forceinline__ void store_tile(const acc_t (&acc)[FM][FN], const ProblemDesc& pd, int m0,
                                                     int n0, int wave_m, int wave_n, char* smem) {
     const int lane = threadIdx.x & 63;
-    if (pd.splits > 1) {
+    if constexpr (SPLIT) {
       split_store(acc, pd, m0, n0, wave_m, wave_n, smem);
       return;
     }
@@ -590,7 +659,8 @@ struct FastTile {
 
   // `before_store` runs once every copy has landed, before the epilogue barrier and the C stores
   // (a global atomic issued there overlaps them instead of delaying the in-order copy waits).
-  template <class Hook>
+  // SPLIT: the unit is one K range of a split-K tile (split_store instead of the C epilogue).
+  template <bool SPLIT, class Hook>
   __device__ static __forceinline__ void run_tile(const ProblemDesc& pd, int tm, int tn, char* smem, bool,
                                                   Hook&& before_store) {
     static_assert(KK % 2 == 0, "fragment double buffer alternates by K step");
@@ -655,7 +725,7 @@ struct FastTile {
     compiler_fence();
     __builtin_amdgcn_s_barrier();
     compiler_fence();
-    store_tile(acc, pd, m0, n0, wave_m, wave_n, smem);
+    store_tile<SPLIT>(acc, pd, m0, n0, wave_m, wave_n, smem);
   }
 
   // Cross-tile chaining of the two-stage tiles.  A workgroup on the static schedule knows its next

@@ -76,6 +76,7 @@ struct KParams {
   // launches); the last unit of a tile sums the partials in split order and stores C.
   int32_t splits;
   int32_t k_chunk;
+  int32_t split_polls;  // polls of a tile's counter a unit makes while waiting for the tile's other units
   float* partials;
   int32_t* counters;
   // Work-stealing schedule (null = static): ticket counters and exit counts, one per 256-byte
@@ -94,6 +95,8 @@ struct ProblemDesc {
   int32_t splits;  // > 1: this unit covers one K range of output tile `tile`
   int32_t split;
   int32_t tile;
+  int32_t split_wait;  // > 0 when every unit of the launch has a workgroup of its own: a tile's units
+                       // may then wait for each other, up to this many polls, to share its reduction
   float* partials;
   int32_t* counters;
 };
@@ -129,6 +132,7 @@ __device__ __forceinline__ void make_uniform(ProblemDesc& pd) {
   pd.splits = uniform(pd.splits);
   pd.split = uniform(pd.split);
   pd.tile = uniform(pd.tile);
+  pd.split_wait = uniform(pd.split_wait);
   pd.partials = uniform(pd.partials);
   pd.counters = uniform(pd.counters);
 }
@@ -506,10 +510,11 @@ struct GemmTile {
 
   // -------------------------------------------------------------------------------------------
   // `before_store` runs once the K loop is done, before the C stores (the work-stealing scheduler
-  // draws its next ticket there).
-  template <class Hook>
+  // draws its next ticket there).  Split-K runs only on the LDS-DMA tiles: SPLIT is never set here.
+  template <bool SPLIT, class Hook>
   __device__ static __forceinline__ void run_tile(const ProblemDesc& pd, int tm, int tn, char* smem, bool tf32,
                                                   Hook&& before_store) {
+    static_assert(!SPLIT, "the general kernel has no split-K epilogue");
     const int wave = threadIdx.x >> 6;
     const int wave_m = wave / WN, wave_n = wave % WN;
     const int m0 = tm * BM, n0 = tn * BN;
@@ -751,7 +756,9 @@ __device__ __forceinline__ void simple_tile(const KParams& p, int t, ProblemDesc
   }
 }
 
-template <class T>
+// SPLIT: the split-K kernel (units are K ranges of tiles, split_store epilogue).  It is a kernel of
+// its own so that the split epilogue's registers do not weigh on the unsplit kernel's loops.
+template <class T, bool SPLIT>
 __global__ void __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WAVES_PER_EU)))
 grouped_gemm_kernel(KParams p) {
   __shared__ __attribute__((aligned(16))) char smem[T::LDS_BYTES];
@@ -767,7 +774,7 @@ grouped_gemm_kernel(KParams p) {
   // Units: tile t, K split u / total_tiles (one split outside split-K launches).  Generic and
   // offsets launches whose groups fit one prefix chunk know their exact tile count on the device
   // (offsets mode gets only an upper bound from the host): the schedules partition that.
-  const int splits = p.splits > 1 ? p.splits : 1;
+  const int splits = SPLIT && p.splits > 1 ? p.splits : 1;
   int units = p.total_tiles * splits;
   if (searched && p.G <= T::PREFIX) units = min(units, s_pref[T::PREFIX] * splits);
   const bool stealing = p.queue != nullptr;
@@ -839,8 +846,8 @@ grouped_gemm_kernel(KParams p) {
   // holds more than one unit ahead, so the last units of a queue still go to whichever workgroups
   // reach them first.  Every ticket is resolved within the tile that drew it, so none is
   // outstanding when the workgroup counts itself out.
-  if constexpr (T::CHAIN_OK) {
-    if (splits == 1 && !p.swiglu &&
+  if constexpr (T::CHAIN_OK && !SPLIT) {
+    if (!p.swiglu &&
         (p.mode == MODE_SINGLE || p.mode == MODE_HOMOGENEOUS || (p.mode == MODE_OFFSETS && p.G <= T::PREFIX)) &&
         (!stealing || T::CHAIN_STEALING) && (p.K + T::BK - 1) / T::BK <= T::CHAIN_MAX_SLICES) {
       auto describe = [&](int unit, ProblemDesc& pd, int& tm, int& tn) {
@@ -852,6 +859,7 @@ grouped_gemm_kernel(KParams p) {
         pd.splits = 1;
         pd.split = 0;
         pd.tile = unit;
+        pd.split_wait = 0;
         pd.partials = p.partials;
         pd.counters = p.counters;
         make_uniform(pd);
@@ -933,6 +941,7 @@ grouped_gemm_kernel(KParams p) {
     pd.splits = splits;
     pd.split = u / p.total_tiles;
     pd.tile = t;
+    pd.split_wait = units <= grid ? p.split_polls : 0;
     pd.partials = p.partials;
     pd.counters = p.counters;
     if (splits > 1) {  // this unit's K range: shift A's columns and B's rows, shorten K
@@ -943,7 +952,7 @@ grouped_gemm_kernel(KParams p) {
     }
     make_uniform(pd);
     int ticket = -1;  // the next unit's ticket: drawn before the C stores, resolved after the tile
-    T::run_tile(pd, uniform(tm), uniform(tn), smem, p.tf32 != 0, [&] {
+    T::template run_tile<SPLIT>(pd, uniform(tm), uniform(tn), smem, p.tf32 != 0, [&] {
       if (stealing && threadIdx.x == 0 && !((tq.drained >> tq.cur) & 1u))
         ticket = atomicAdd(tq.q + tq.cur * kQueueStride, 1);
     });

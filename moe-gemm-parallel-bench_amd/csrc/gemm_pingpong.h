@@ -52,7 +52,7 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
   static_assert(Base::IA % NW == 0 && Base::IB % NW == 0, "every wave issues the same number of copies");
   static_assert(STAGES >= 3, "group 1 needs at least one phase between issuing and publishing a slice");
 
-  template <class Hook>
+  template <bool SPLIT, class Hook>
   __device__ static __forceinline__ void run_tile(const ProblemDesc& pd, int tm, int tn, char* smem, bool,
                                                   Hook&& before_store) {
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -99,10 +99,10 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
     // stage C in the wave's own LDS slots; then the hook, as in FastTile.
     wait_vmcnt<0>();
     before_store();
-    if (pd.splits > 1) {
+    if constexpr (SPLIT) {
       // The split epilogue has workgroup barriers of its own: align the groups first.
       if (!second) phase_barrier();
-      Base::store_tile(acc, pd, m0, n0, wave_m, wave_n, smem);
+      Base::template store_tile<true>(acc, pd, m0, n0, wave_m, wave_n, smem);
     } else if (!second) {
       Base::store_tile(acc, pd, m0, n0, wave_m, wave_n, smem);
       phase_barrier();

@@ -22,11 +22,12 @@ struct KernelEntry {
   int swiglu_ok;   // the fast path can run the packed Gate+Up SwiGLU epilogue (even FN)
   LaunchFn launch_fast;     // null when the dtype has no fast path
   LaunchFn launch_general;
+  LaunchFn launch_fast_split;  // the fast path's split-K kernel (null without a fast path)
 };
 
-template <class T>
+template <class T, bool SPLIT = false>
 hipError_t launch_tile(const KParams& p, int grid, hipStream_t stream) {
-  hipLaunchKernelGGL(grouped_gemm_kernel<T>, dim3(grid), dim3(T::NT), 0, stream, p);
+  hipLaunchKernelGGL((grouped_gemm_kernel<T, SPLIT>), dim3(grid), dim3(T::NT), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -48,22 +49,24 @@ template <class E, int BM, int BN, int BK, int WM, int WN, int S>
 struct GemmTileEntry : GemmTile<E, BM, BN, BK, WM, WN> {};
 #define MOEGEMM_GEN(E, BM, BN, BK, WM, WN, S) GemmTileEntry<E, BM, BN, BK, WM, WN, S>
 
-#define MOEGEMM_INST16(E, BM, BN, BK, WM, WN, S)                                              \
-  template __global__ void grouped_gemm_kernel<MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S)>(KParams); \
-  template __global__ void grouped_gemm_kernel<MOEGEMM_GEN(E, BM, BN, BK, WM, WN, S)>(KParams);
+#define MOEGEMM_INST16(E, BM, BN, BK, WM, WN, S)                                                     \
+  template __global__ void grouped_gemm_kernel<MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S), false>(KParams); \
+  template __global__ void grouped_gemm_kernel<MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S), true>(KParams);  \
+  template __global__ void grouped_gemm_kernel<MOEGEMM_GEN(E, BM, BN, BK, WM, WN, S), false>(KParams);
 #define MOEGEMM_ENTRY16(E, BM, BN, BK, WM, WN, S)                                             \
   KernelEntry{E::dtype, BM, BN, BK, (WM) * (WN), S, WM, WN,                                   \
               MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S)::LDS_BYTES,                              \
               MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S)::SWIGLU_OK ? 1 : 0,                      \
               &launch_tile<MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S)>,                          \
-              &launch_tile<MOEGEMM_GEN(E, BM, BN, BK, WM, WN, S)>},
+              &launch_tile<MOEGEMM_GEN(E, BM, BN, BK, WM, WN, S)>,                           \
+              &launch_tile<MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S), true>},
 
 #define MOEGEMM_INST32(E, BM, BN, BK, WM, WN, S) \
-  template __global__ void grouped_gemm_kernel<MOEGEMM_GEN(E, BM, BN, BK, WM, WN, S)>(KParams);
+  template __global__ void grouped_gemm_kernel<MOEGEMM_GEN(E, BM, BN, BK, WM, WN, S), false>(KParams);
 #define MOEGEMM_ENTRY32(E, BM, BN, BK, WM, WN, S)                                             \
   KernelEntry{E::dtype, BM, BN, BK, (WM) * (WN), S, WM, WN,                                   \
               MOEGEMM_GEN(E, BM, BN, BK, WM, WN, S)::LDS_BYTES, 0, nullptr,                      \
-              &launch_tile<MOEGEMM_GEN(E, BM, BN, BK, WM, WN, S)>},
+              &launch_tile<MOEGEMM_GEN(E, BM, BN, BK, WM, WN, S)>, nullptr},
 
 // 16-bit menu (bf16 and f16 share it): large-M MFMA-bound tiles down to skinny-M streaming tiles.
 // STAGES is sized to the 160 KiB LDS of a CU; the 2-stage narrow tiles at the end fit two

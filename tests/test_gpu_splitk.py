@@ -180,3 +180,49 @@ def test_every_tile_split_known_answer_with_tails(splits):
         torch.cuda.synchronize()
         assert last_matmul_split() == splits
         assert torch.equal(c.double().cpu(), exact), f"tile {cfg.tile_key} splits {splits}"
+
+
+@pytest.mark.parametrize("polls", [None, "1", "0"], ids=["polls_default", "polls_1", "polls_0"])
+@pytest.mark.parametrize("tile", [(256, 256, 32, 8, 4), (128, 256, 64, 8, 3), (64, 128, 64, 4, 4),
+                                  (16, 64, 128, 4, 4)], ids=lambda t: "x".join(map(str, t)))
+def test_split_reduction_same_bits_whoever_reduces(tile, polls, monkeypatch):
+    """The units of a tile share its reduction when every unit has a workgroup of its own (grid >=
+    units) and the partials are large; on smaller grids a workgroup runs several units and the last
+    unit of each tile reduces it alone.  A unit waits for its partners only a bounded number of
+    polls (MOEGEMM_SPLIT_POLLS; 1 makes units stop waiting often, so the last unit to arrive takes
+    over their slices; 0 never waits).  Every element sums the partials in split order whoever
+    reduces it, so all grids and poll limits give the same bits, close to the oracle, and every
+    launch leaves the workspace counters at zero."""
+    from kernels import _native
+
+    if polls is None:
+        monkeypatch.delenv("MOEGEMM_SPLIT_POLLS", raising=False)
+    else:
+        monkeypatch.setenv("MOEGEMM_SPLIT_POLLS", polls)
+
+    bm, bn, bk, warps, stages = tile
+    m, k, n = 2 * bm + 44, 4096, 2 * bn + 8
+    a = (torch.randn((m, k), device="cuda") / math.sqrt(k)).to(torch.bfloat16)
+    b = torch.randn((k, n), device="cuda").to(torch.bfloat16)
+    tiles = -(-m // bm) * -(-n // bn)
+    lib = _native.library()
+    stream = _native.current_stream_handle(a.device)
+    for splits in (3, 4):
+        nbytes = _native.splitk_workspace_bytes(tiles, splits, bm, bn)
+        workspace = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+        outputs = []
+        for grid in (0, 1, 5, tiles * splits - 1):
+            print(f"splitk whoever reduces tile={tile} polls={polls} splits={splits} grid={grid}", flush=True)
+            c = torch.full((m, n), float("nan"), device="cuda", dtype=torch.bfloat16)
+            _native.check(lib.moegemm_matmul_splitk(
+                a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, a.stride(0), a.stride(1), b.stride(0),
+                b.stride(1), c.stride(0), c.stride(1), _native.DTYPE_BF16, bm, bn, bk, 8, warps, stages, splits,
+                grid, workspace.data_ptr(), workspace.numel(), stream))
+            torch.cuda.synchronize()
+            assert not workspace[:256 * 1024].any(), f"counters not re-armed (grid {grid})"
+            outputs.append(c)
+        for grid, c in zip((1, 5, tiles * splits - 1), outputs[1:]):
+            assert torch.equal(c, outputs[0]), f"splits {splits} grid {grid} differs from grid = units"
+        assert normwise(outputs[0], a.float() @ b.float()) <= 1e-2
+        rows = slice(m - 3, m)
+        assert normwise(outputs[0][rows], oracle_product(a[rows], b)) <= 1e-2
