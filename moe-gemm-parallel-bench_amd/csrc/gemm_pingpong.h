@@ -53,11 +53,21 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
   static_assert(STAGES >= 3, "group 1 needs at least one phase between issuing and publishing a slice");
 
   template <bool SPLIT, class Hook>
-  __device__ static __forceinline__ void run_tile(const ProblemDesc& pd, int tm, int tn, char* smem, bool,
+  __device__ static __forceinline__ void run_tile(const ProblemDesc& pd, int tm, int tn, char* smem, bool tf32,
                                                   Hook&& before_store) {
+    // Each group runs a copy of the schedule compiled for it (no group tests inside the K loop).
+    if (__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) >= NW / 2)
+      group_tile<SPLIT, true>(pd, tm, tn, smem, before_store);
+    else
+      group_tile<SPLIT, false>(pd, tm, tn, smem, before_store);
+  }
+
+  template <bool SPLIT, bool SECOND, class Hook>
+  __device__ static __forceinline__ void group_tile(const ProblemDesc& pd, int tm, int tn, char* smem,
+                                                    Hook&& before_store) {
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int wave_m = wave / WN, wave_n = wave % WN;
-    const bool second = wave >= NW / 2;
+    constexpr bool second = SECOND;
     const int m0 = tm * BM, n0 = tn * BN;
     Dma d;
     Base::setup_dma(d, pd, m0, n0, smem);
@@ -75,7 +85,7 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
     for (int s = 0; s < STAGES; ++s) Base::issue_stage(d, s, s * BK);
     wait_vmcnt<(STAGES - 1) * XMIN>();
     phase_barrier();
-    if (second) phase_barrier();  // group 1 runs one barrier behind
+    if constexpr (second) phase_barrier();  // group 1 runs one barrier behind
 
     i16x8_t af[KK][FM], bf[KK][FN];
     const int kt_count = (pd.k + BK - 1) / BK;
@@ -87,12 +97,12 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
       for (int kk = 0; kk < KK; ++kk)
         Base::load_frags(af[kk], bf[kk], cur, cur + A_BYTES, kk, wave_m, wave_n, pd.swiglu != 0);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      if (second) wait_vmcnt<(STAGES - 2) * XMIN>();
+      if constexpr (second) wait_vmcnt<(STAGES - 2) * XMIN>();
       phase_barrier();
       // Compute phase.
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) Base::template mfma_rows<0, FM>(acc, af[kk], bf[kk]);
-      if (!second) wait_vmcnt<(STAGES - 2) * XMIN>();
+      if constexpr (!second) wait_vmcnt<(STAGES - 2) * XMIN>();
       phase_barrier();
     }
     // This wave's remaining copies (zero-filled slices past K) land before the epilogue, which may
@@ -101,13 +111,11 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
     before_store();
     if constexpr (SPLIT) {
       // The split epilogue has workgroup barriers of its own: align the groups first.
-      if (!second) phase_barrier();
+      if constexpr (!second) phase_barrier();
       Base::template store_tile<true>(acc, pd, m0, n0, wave_m, wave_n, smem);
-    } else if (!second) {
-      Base::store_tile(acc, pd, m0, n0, wave_m, wave_n, smem);
-      phase_barrier();
     } else {
       Base::store_tile(acc, pd, m0, n0, wave_m, wave_n, smem);
+      if constexpr (!second) phase_barrier();
     }
   }
 
@@ -140,9 +148,19 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
   __device__ static __forceinline__ bool run_tile_chained(const ProblemDesc& pd, int tm, int tn, char* smem, Chain& ch,
                                                           Sched& sched, ProblemDesc& next, int& ntm, int& ntn) {
     static_assert(CHAIN_OK, "the chained epilogue stages C in one stage's slots");
+    // Each group runs a copy of the tile's schedule compiled for it, so the group tests of the K
+    // steps (which wait comes where, the extra barriers) cost no branches.
+    if (__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) >= NW / 2)
+      return chained_group<true>(pd, tm, tn, smem, ch, sched, next, ntm, ntn);
+    return chained_group<false>(pd, tm, tn, smem, ch, sched, next, ntm, ntn);
+  }
+
+  template <bool SECOND, class Sched>
+  __device__ static __forceinline__ bool chained_group(const ProblemDesc& pd, int tm, int tn, char* smem, Chain& ch,
+                                                       Sched& sched, ProblemDesc& next, int& ntm, int& ntn) {
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int wave_m = wave / WN, wave_n = wave % WN;
-    const bool second = wave >= NW / 2;
+    constexpr bool second = SECOND;
     const int m0 = tm * BM, n0 = tn * BN;
     Dma d;
     Base::setup_dma(d, pd, m0, n0, smem);
@@ -166,7 +184,7 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
       wait_vmcnt<(STAGES - 1) * XMIN>();
     }
     phase_barrier();
-    if (second) phase_barrier();  // group 1 runs one barrier behind
+    if constexpr (second) phase_barrier();  // group 1 runs one barrier behind
     sched.started();
     const bool has_next = sched.next(next, ntm, ntn);
     const int kt_count = (pd.k + BK - 1) / BK;
@@ -210,12 +228,12 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
           wait_vmcnt<(STAGES - 2) * XMIN>();
         }
       };
-      if (second) wait_next();
+      if constexpr (second) wait_next();
       phase_barrier();
       // Compute phase.
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) Base::template mfma_rows<0, FM>(acc, af[kk], bf[kk]);
-      if (!second) wait_next();
+      if constexpr (!second) wait_next();
       phase_barrier();
     };
     using no_issue = std::integral_constant<int, 0>;
@@ -234,17 +252,13 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
         Base::setup_dma(dn, next, ntm * BM, ntn * BN, smem);
         Base::issue_stage(dn, last, (STAGES - 1) * BK);
       }
-      if (!second) phase_barrier();
+      if constexpr (!second) phase_barrier();
       ch.rot = (kt_count + rot) & (STAGES - 1);
       ch.prefetched = true;
     } else {
       wait_vmcnt<0>();
-      if (!second) {
-        Base::store_tile(acc, pd, m0, n0, wave_m, wave_n, smem);
-        phase_barrier();
-      } else {
-        Base::store_tile(acc, pd, m0, n0, wave_m, wave_n, smem);
-      }
+      Base::store_tile(acc, pd, m0, n0, wave_m, wave_n, smem);
+      if constexpr (!second) phase_barrier();
       ch.prefetched = false;
     }
     return has_next;
