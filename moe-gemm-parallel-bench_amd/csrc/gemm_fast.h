@@ -741,13 +741,27 @@ struct FastTile {
   // made them spill (the 8-wave 256x256x64 tile from 7 to about 200 spilled VGPRs).  Tiles with
   // more than 64 accumulator registers per wave chain only short-K launches (CHAIN_MAX_SLICES):
   // 64x512x64 gained 8 % at K = 256 (4 slices) and lost 2-3 % at K = 2048 (32 slices).
-  static constexpr bool CHAIN_OK = STAGES == 2 && FM * FN * ACC <= 128 && BM * BN <= 32768;
-  static constexpr int CHAIN_MAX_SLICES = FM * FN * ACC <= 64 ? (1 << 30) : 8;
-  static constexpr bool CHAIN_STEALING = true;  // the chained loop also runs the stealing schedule
+  //
+  // Four-stage tiles of at most 32768 outputs and 64 accumulator registers per wave chain deeper,
+  // on the static schedule (run_tile_chained_deep): the last STAGES - 1 refills of a tile fetch the
+  // next tile's slices 0 .. STAGES - 2, and its slice STAGES - 1 follows the C stores, so the next
+  // tile starts with STAGES slices in flight as an unchained tile's prologue would have them.  A
+  // two-stage tile can prefetch only one slice, which leaves one slice's memory latency exposed at
+  // every tile: short-K launches (DSV3 TP W2, K = 256, four 64-deep slices per tile) paid it 4 times
+  // per 4 slices.
+  // Deep chaining is kept to launches of STAGES to 8 slices: with fewer the tile has no slice
+  // boundary to prefetch from, and on long-K launches (32 slices) it measured 1-2 % slower than
+  // run_tile's own prologue.
+  static constexpr bool CHAIN_DEEP = STAGES == 4 && FM * FN * ACC <= 64 && BM * BN <= 32768;
+  static constexpr bool CHAIN_OK = (STAGES == 2 && FM * FN * ACC <= 128 && BM * BN <= 32768) || CHAIN_DEEP;
+  static constexpr int CHAIN_MIN_SLICES = CHAIN_DEEP ? STAGES : 1;
+  static constexpr int CHAIN_MAX_SLICES = CHAIN_DEEP ? 8 : FM * FN * ACC <= 64 ? (1 << 30) : 8;
+  static constexpr bool CHAIN_STEALING = STAGES == 2;  // the two-stage loop also runs the stealing schedule
   static constexpr int CH_ROWS_FIT = STAGED_OK ? (XMIN * 1024 / ROWB) / MI * MI : MI;
   static constexpr int CH_ROWS = CH_ROWS_FIT < WTM ? CH_ROWS_FIT : WTM;  // staged rows per round
   static constexpr int CHAIN_STORES = STAGED_OK ? WTM * ROWB / 1024 : FM * FN * (ACC / 4);
-  static_assert(!CHAIN_OK || CHAIN_STORES + QA + QB < 64, "outstanding operations must fit the 6-bit vmcnt");
+  static_assert(!CHAIN_OK || CHAIN_STORES + (STAGES - 1) * (QA + QB) < 64,
+                "outstanding operations must fit the 6-bit vmcnt");
   static_assert(!(CHAIN_OK && STAGED_OK) || (CH_ROWS > 0 && WTM % CH_ROWS == 0 && (CH_ROWS * ROWB) % 1024 == 0),
                 "staging rounds must cover the wave tile in whole slots");
   struct Chain {
@@ -830,6 +844,136 @@ struct FastTile {
     }
   }
 
+  // run_tile's schedule with deep cross-tile chaining (CHAIN_DEEP tiles, static schedule).  The K
+  // loop is run_tile's.  In buffer terms, slice kt of a tile lives in buffer (kt + rot) % STAGES,
+  // where rot is where the previous tile left the next tile's slice 0.  Once the next tile is known
+  // (at the prologue barrier), the refill that would copy slice kt + STAGES of this tile when that
+  // lies past K copies the next tile's slice kt + STAGES - kt_count instead: slices 0 .. STAGES - 2
+  // of the next tile, at the last STAGES - 1 slice boundaries.  The last slice has no boundary: its
+  // MFMAs run, every wave reads its buffer to the end (a barrier), C leaves through the wave's slots
+  // there in CHAIN_STORES counted stores, and each wave then copies the next tile's slice
+  // STAGES - 1 into its own slots of that buffer.  A wave's vector memory operations complete in
+  // issue order, so the next tile's wait for its slice j counts the younger slices plus, for
+  // j <= STAGES - 2, the stores issued after them: it never waits for the stores themselves before
+  // slice STAGES - 1 is needed.  Tiles of fewer than STAGES slices, the workgroup's last tile, and C
+  // that is not 16-byte aligned (staged tiles) use run_tile's zero slices and unchained epilogue.
+  template <class Sched>
+  __device__ static __forceinline__ bool run_tile_chained_deep(const ProblemDesc& pd, int tm, int tn, char* smem,
+                                                               Chain& ch, Sched& sched, ProblemDesc& next, int& ntm,
+                                                               int& ntn) {
+    static_assert(CHAIN_DEEP && (STAGES & (STAGES - 1)) == 0, "buffer rotation needs a power-of-two ring");
+    static_assert(KK % 2 == 0, "fragment double buffer alternates by K step");
+    constexpr int S = STAGES;
+    constexpr int HALF = FM / 2 > 0 ? FM / 2 : 1;
+    constexpr int NDS = FM + 2 * FN;
+    constexpr int NVM = QA + QB;
+    const int wave = threadIdx.x >> 6;
+    const int wave_m = wave / WN, wave_n = wave % WN;
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    acc_t acc[FM][FN];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int i = 0; i < ACC; ++i) acc[fm][fn][i] = 0.0f;
+
+    Dma d;
+    setup_dma(d, pd, m0, n0, smem);
+    const bool pre = ch.prefetched;
+    const int rot = uniform(pre ? ch.rot : 0);  // buffer indices are wave-uniform (LDS-DMA's M0)
+    if (pre) {
+      // In flight: slices 0 .. S-2, the previous tile's CHAIN_STORES stores, slice S-1.
+      wait_vmcnt<(S - 1) * XMIN + CHAIN_STORES>();
+    } else {
+#pragma unroll
+      for (int st = 0; st < S; ++st) issue_stage(d, st, st * BK);
+      wait_vmcnt<(S - 1) * XMIN>();
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    compiler_fence();
+    __builtin_amdgcn_s_barrier();
+    compiler_fence();
+    sched.started();
+    sched.before_barrier();
+    const bool has_next = sched.next(next, ntm, ntn);
+    const int kt_count = (pd.k + BK - 1) / BK;
+    const bool c16 = ((reinterpret_cast<uintptr_t>(pd.c) & 15) == 0) && (pd.scm & 7) == 0;
+    const bool chain = has_next && kt_count >= S && (!STAGED_OK || c16);
+    i16x8_t af[2][FM], bf[2][FN];
+    load_frags(af[0], bf[0], smem + rot * STAGE_BYTES, smem + rot * STAGE_BYTES + A_BYTES, 0, wave_m, wave_n, false);
+
+    for (int kt = 0; kt < kt_count; ++kt) {
+      const int b = uniform((kt + rot) & (S - 1));
+      const char* cur = smem + b * STAGE_BYTES;
+      const char* nxt = smem + ((b + 1) & (S - 1)) * STAGE_BYTES;
+#pragma unroll
+      for (int kk = 0; kk < KK - 1; ++kk) {
+        load_frags(af[(kk + 1) & 1], bf[(kk + 1) & 1], cur, cur + A_BYTES, kk + 1, wave_m, wave_n, false);
+        mfma_rows<0, FM>(acc, af[kk & 1], bf[kk & 1]);
+        interleave<FM * FN, NDS, 0>();
+      }
+      constexpr int L = (KK - 1) & 1;
+      if (!chain || kt + 1 < kt_count) {
+        mfma_rows<0, HALF>(acc, af[L], bf[L]);
+        // Slice kt + 1 complete: younger are slices kt + 2 .. kt + S - 1, plus the previous tile's
+        // stores while slice kt + 1 is one of the first S - 1 prefetched slices.
+        if (pre && kt + 1 <= S - 2)
+          wait_vmcnt<(S - 2) * XMIN + CHAIN_STORES>();
+        else
+          wait_vmcnt<(S - 2) * XMIN>();
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        compiler_fence();
+        __builtin_amdgcn_s_barrier();
+        compiler_fence();
+        const int st = kt + S;
+        if (chain && st >= kt_count) {
+          Dma dn;  // the next tile's copy state, recomputed for each of its prefetched slices
+          setup_dma(dn, next, ntm * BM, ntn * BN, smem);
+          issue_stage(dn, b, (st - kt_count) * BK);
+        } else {
+          issue_stage(d, b, st * BK);
+        }
+        load_frags(af[0], bf[0], nxt, nxt + A_BYTES, 0, wave_m, wave_n, false);
+        mfma_rows<HALF, FM>(acc, af[L], bf[L]);
+        interleave<(FM - HALF) * FN, NDS, NVM>();
+      } else {
+        mfma_rows<0, FM>(acc, af[L], bf[L]);  // the last slice of a chained tile
+      }
+    }
+    if (chain) {
+      const int last = uniform((kt_count - 1 + rot) & (S - 1));
+      // Every wave has read the last slice's buffer before any stages C in its slots there.
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      compiler_fence();
+      __builtin_amdgcn_s_barrier();
+      compiler_fence();
+      if constexpr (STAGED_OK)
+        staged_store_counted(acc, pd, m0, n0, wave_m, wave_n, smem, last);
+      else
+        store_tile_counted(acc, pd, m0, n0, wave_m, wave_n);
+      {
+        Dma dn;
+        setup_dma(dn, next, ntm * BM, ntn * BN, smem);
+        issue_stage(dn, last, (S - 1) * BK);
+      }
+      ch.rot = (kt_count + rot) & (S - 1);
+      ch.prefetched = true;
+    } else {
+      // Copies of this tile (zero slices past K) landed and every wave is done with LDS before
+      // the next tile's own prologue refills it.
+      wait_vmcnt<0>();
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      compiler_fence();
+      __builtin_amdgcn_s_barrier();
+      compiler_fence();
+      store_tile(acc, pd, m0, n0, wave_m, wave_n, smem);
+      ch.prefetched = false;
+    }
+    return has_next;
+  }
+
   // run_tile's schedule for CHAIN_OK tiles.  `ch` carries the prefetch from one call to the next;
   // start a workgroup with ch.prefetched false.  The workgroup's next tile comes from `sched`, whose
   // hooks every wave runs once per tile, in this order:
@@ -847,7 +991,8 @@ struct FastTile {
   template <class Sched>
   __device__ static __forceinline__ bool run_tile_chained(const ProblemDesc& pd, int tm, int tn, char* smem, Chain& ch,
                                                           Sched& sched, ProblemDesc& next, int& ntm, int& ntn) {
-    static_assert(CHAIN_OK, "the chained schedule is for two-stage tiles");
+    if constexpr (CHAIN_DEEP) return run_tile_chained_deep(pd, tm, tn, smem, ch, sched, next, ntm, ntn);
+    static_assert(CHAIN_OK, "the chained schedule is for two-stage and four-stage tiles");
     static_assert(KK % 2 == 0, "fragment double buffer alternates by K step");
     constexpr int HALF = FM / 2 > 0 ? FM / 2 : 1;
     constexpr int NDS = FM + 2 * FN;

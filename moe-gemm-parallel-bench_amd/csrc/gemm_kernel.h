@@ -849,7 +849,8 @@ grouped_gemm_kernel(KParams p) {
   if constexpr (T::CHAIN_OK && !SPLIT) {
     if (!p.swiglu &&
         (p.mode == MODE_SINGLE || p.mode == MODE_HOMOGENEOUS || (p.mode == MODE_OFFSETS && p.G <= T::PREFIX)) &&
-        (!stealing || T::CHAIN_STEALING) && (p.K + T::BK - 1) / T::BK <= T::CHAIN_MAX_SLICES) {
+        (!stealing || T::CHAIN_STEALING) && (p.K + T::BK - 1) / T::BK <= T::CHAIN_MAX_SLICES &&
+        (p.K + T::BK - 1) / T::BK >= T::CHAIN_MIN_SLICES) {
       auto describe = [&](int unit, ProblemDesc& pd, int& tm, int& tn) {
         if (p.mode == MODE_OFFSETS)
           searched_tile<T>(p, s_pref, 0, unit, pd, tm, tn);

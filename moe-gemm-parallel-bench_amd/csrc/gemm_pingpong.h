@@ -135,6 +135,7 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
   // 16-byte aligned run the unchained epilogue (zero slices, wait for every copy).  The next unit
   // is computed right after the prologue barrier: only the static schedule is served here.
   static constexpr bool CHAIN_OK = Base::STAGED_OK && (STAGES & (STAGES - 1)) == 0;
+  static constexpr int CHAIN_MIN_SLICES = 1;
   static constexpr int CHAIN_MAX_SLICES = 1 << 30;
   static constexpr bool CHAIN_STEALING = false;
   static constexpr int CHAIN_STORES = Base::CHAIN_STORES;

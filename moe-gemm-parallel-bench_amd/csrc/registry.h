@@ -82,7 +82,8 @@ struct GemmTileEntry : GemmTile<E, BM, BN, BK, WM, WN> {};
   X(E, 16, 256, 64, 1, 4, 4) X(E, 16, 256, 128, 1, 4, 2) X(E, 16, 128, 128, 1, 4, 4)         \
   X(E, 16, 64, 128, 1, 4, 4) X(E, 16, 64, 128, 1, 4, 7)                                    \
   X(E, 16, 256, 64, 1, 4, 2) X(E, 32, 256, 64, 1, 4, 2) X(E, 64, 128, 64, 2, 2, 2)        \
-  X(E, 16, 128, 64, 1, 4, 2) X(E, 16, 512, 64, 1, 4, 2) X(E, 64, 512, 64, 1, 4, 2)
+  X(E, 16, 128, 64, 1, 4, 2) X(E, 16, 512, 64, 1, 4, 2) X(E, 64, 512, 64, 1, 4, 2)        \
+  X(E, 32, 512, 32, 1, 4, 4)
 
 // fp32 menu (general kernel, v_mfma_f32_16x16x4_f32); STAGES is the register-staged double buffer.
 #define MOEGEMM_MENU_F32(X, E)                                                               \

@@ -55,6 +55,7 @@ _MENU_16BIT: tuple[tuple[int, int, int, int, int], ...] = (
     (16, 64, 128, 4, 4), (16, 64, 128, 4, 7),
     (16, 256, 64, 4, 2), (32, 256, 64, 4, 2), (64, 128, 64, 4, 2), (16, 128, 64, 4, 2),
     (16, 512, 64, 4, 2), (64, 512, 64, 4, 2),
+    (32, 512, 32, 4, 4),
 )
 _MENU_F32: tuple[tuple[int, int, int, int, int], ...] = (
     (128, 128, 32, 4, 2), (64, 64, 32, 4, 2), (32, 64, 32, 4, 2),
