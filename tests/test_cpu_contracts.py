@@ -162,6 +162,11 @@ def test_large_single_gemms_measure_the_eight_wave_256_tiles_first():
 def test_grouped_candidates_cover_the_workload_families():
     skinny = grouped_candidate_configs(8, 4096, 7168, problem_count=32, sm_count=256)
     assert {c.block_m for c in skinny} <= {16, 32}
+    # Decode groups (M_e <= 16) time 32-row tiles next to the 16-row ones: the 32x512x32
+    # four-stage tile is the measured best on DSV3 EP W2 at M_e = 8.
+    decode = grouped_candidate_configs(8, 7168, 2048, problem_count=32, sm_count=256, dtype=torch.bfloat16)
+    assert {c.block_m for c in decode} == {16, 32}
+    assert any(c.tile_key == (32, 512, 32, 4, 4) for c in decode)
     wide = grouped_candidate_configs(512, 4096, 7168, problem_count=32, sm_count=256)
     assert any(c.block_m == 256 and c.block_n == 256 for c in wide)
     assert {c.cta_multiplier for c in wide} >= {1, 2}
