@@ -2,7 +2,7 @@
 
 ``python bench.py [--gpus 1] [--steps K] [--warmup W]`` prints ONE JSON line.
 
-* Workload (one EP rank of BASELINE configs[2], the north-star target case): 32 experts of
+* Workload (one EP rank of BASELINE.json configs[2], the north-star target case): 32 experts of
   [512, 7168] @ [7168, 4096] in bf16 with fp32 accumulation, synthetic ``normal_() * 0.1`` inputs
   resident in HBM.  A step is one ``launch_grouped`` call over the whole group (one kernel launch).
 * ``value`` is whole-job TFLOP/s = 2 * sum_e M_e*K*N / (time per step), from HIP events recorded on
@@ -45,7 +45,7 @@ METRIC = "grouped-GEMM TFLOP/s + % MFMA/HBM roofline, EP vs TP per-rank, 1 MI355
 
 # DeepSeek-V3: H=7168, F=2048, E=256, topk=8, P=8.
 DSV3 = dict(hidden=7168, ffn=2048, experts=256, parallel=8)
-# The BASELINE models for `--case` runs (profiles): name -> (H, F, E, P, dtype name).
+# The BASELINE.json models for `--case` runs (profiles): name -> (H, F, E, P, dtype name).
 MODELS = {"dsv3": (7168, 2048, 256, 8, "bf16"), "mixtral": (4096, 14336, 8, 8, "bf16"),
           "qwen3": (2048, 768, 128, 4, "fp16")}
 
@@ -130,7 +130,7 @@ def _timed(step, steps: int, warmup: int, settle_s: float = 0.0) -> tuple[float,
 
 def _case(projection: str, parallel_type: str, m: int, steps: int, warmup: int, seed: int = 1234,
           pinned=None, model: str = "dsv3", settle_s: float = 0.0) -> dict:
-    """Time one case of a BASELINE model (DSV3 by default); ``pinned`` (a KernelConfig) skips autotuning."""
+    """Time one case of a BASELINE.json model (DSV3 by default); ``pinned`` (a KernelConfig) skips autotuning."""
     import torch
 
     from kernels.grouped_gemm import launch_grouped

@@ -4,7 +4,7 @@ The vectors are independent of the oracle: inputs are drawn with a seeded torch 
 (``normal_() * 0.1`` like the reference builders, kernels/grouped_gemm.py:522-527), rounded to
 the operand dtype by torch, and the expected values are torch's float64 matmul of those rounded
 operands plus torch's cast of that product to the operand dtype.  Shapes follow the reference's
-own GPU tests (tests/test_gpu.py:74, :89, :100, :178) plus a BASELINE plumbing-case sample.
+own GPU tests (tests/test_gpu.py:74, :89, :100, :178) plus a BASELINE.json plumbing-case sample.
 
 Run from the repository root:  python tests/golden/make_golden.py
 """
@@ -50,7 +50,7 @@ def main() -> None:
     # Packed W13 (gate | up along N): reference tests/test_gpu.py:176-188 shape.
     a, b, exact, rounded = case(gen, 17, 13, 62, torch.float16)
     arrays["w13_fp16_a"], arrays["w13_fp16_b"], arrays["w13_fp16_exact"], arrays["w13_fp16_out"] = a, b, exact, rounded
-    # Plumbing case sample (BASELINE configs[0]): one expert of [64, 512] @ [512, 1024], bf16,
+    # Plumbing case sample (BASELINE.json configs[0]): one expert of [64, 512] @ [512, 1024], bf16,
     # N(0,1)/sqrt(K) inputs; the exact product is kept only for 64 sampled entries.
     k = 512
     a = (torch.empty((64, k), dtype=torch.float64).normal_(generator=gen) / math.sqrt(k)).to(torch.bfloat16)

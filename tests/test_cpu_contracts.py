@@ -103,7 +103,7 @@ def test_ep_tp_shapes_split_the_intended_dimension():
 
 
 def test_baseline_config_shapes():
-    # BASELINE configs: Mixtral P=8, Qwen3-30B-A3B P=4.
+    # BASELINE.json configs: Mixtral P=8, Qwen3-30B-A3B P=4.
     assert moe_shapes("W1", "EP", 16, 4096, 14336, 8, 8) == [(16, 4096, 28672)]
     assert moe_shapes("W2", "TP", 16, 4096, 14336, 8, 8) == [(16, 1792, 4096)] * 8
     assert moe_shapes("W1", "TP", 4, 2048, 768, 128, 4) == [(4, 2048, 384)] * 128

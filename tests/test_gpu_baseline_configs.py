@@ -1,6 +1,6 @@
-"""GPU tests at the BASELINE configurations' full per-rank sizes, plus graph capture and timing.
+"""GPU tests at the BASELINE.json configurations' full per-rank sizes, plus graph capture and timing.
 
-Full-size checks, on all 36 MoE cases of BASELINE configs[1..3], use properties that do not depend
+Full-size checks, on all 36 MoE cases of BASELINE.json configs[1..3], use properties that do not depend
 on size:
   * exact-integer known answers on every expert (A = 1, B_e = e + 1 => C_e = K (e + 1), exact in
     the fp32 accumulator and representable in bf16/fp16 for these K) - catches any wrong index,
@@ -25,7 +25,7 @@ pytestmark = pytest.mark.gpu
 
 NORMWISE = {torch.bfloat16: 1e-2, torch.float16: 2e-3}
 
-# Every MoE case of BASELINE configs[1..3]: 3 models x {W1, W2} x {EP, TP} x their M_e sweep, as
+# Every MoE case of BASELINE.json configs[1..3]: 3 models x {W1, W2} x {EP, TP} x their M_e sweep, as
 # (name, projection, parallel, M_e, H, F, E, P, dtype).
 _MODELS = (("dsv3", (8, 64, 512), 7168, 2048, 256, 8, torch.bfloat16),
            ("mixtral", (16, 128, 1024), 4096, 14336, 8, 8, torch.bfloat16),
@@ -95,7 +95,7 @@ def test_full_size_random_sampled_against_references(case):
     assert normwise(c[rows], oracle_product(a[rows], b)) <= NORMWISE[dtype]
 
 
-# The value distributions BASELINE configs[1] and configs[3] state for their inputs and weights:
+# The value distributions BASELINE.json configs[1] and configs[3] state for their inputs and weights:
 # Mixtral-8x7B N(0, 0.02), Qwen3-30B-A3B U(-1, 1) * 0.05.
 _STATED = {"mixtral": lambda t, g: t.normal_(0.0, 0.02, generator=g),
            "qwen3": lambda t, g: t.uniform_(-1.0, 1.0, generator=g).mul_(0.05)}

@@ -3,7 +3,7 @@
 Mirrors the reference's tests/test_gpu.py cases (odd shapes in three dtypes, strided fp32/TF32,
 heterogeneous distinct pointers, homogeneous fast path, exact-integer known answers for every
 candidate, multi-round persistent grid with NaN guard bands, packed W13, G == 1 dispatch) and
-adds the BASELINE shapes.  Tolerances: exact integers are compared bit for bit; random inputs
+adds the BASELINE.json shapes.  Tolerances: exact integers are compared bit for bit; random inputs
 use the reference's per-dtype ``assert_close`` and the normwise bound max|C - R| / max|R|
 (bf16 <= 1e-2, fp16 <= 2e-3, fp32 <= 1e-5) against the oracle's fp64-accumulated product.
 """
@@ -202,7 +202,7 @@ def test_one_problem_group_dispatches_standard_matmul():
 
 
 def test_plumbing_case_bf16_against_oracle():
-    """BASELINE configs[0]: 8 experts of [64, 512] @ [512, 1024], bf16, N(0,1)/sqrt(K) inputs."""
+    """BASELINE.json configs[0]: 8 experts of [64, 512] @ [512, 1024], bf16, N(0,1)/sqrt(K) inputs."""
     from kernels.grouped_gemm import launch_grouped, workspace_from_tensors
 
     g, m, k, n = 8, 64, 512, 1024
