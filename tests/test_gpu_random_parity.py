@@ -1,12 +1,13 @@
 """Randomised exact-integer parity sweep over the launch modes, tiles, grids, schedules and splits.
 
-Each case draws a dtype (bf16 or fp16), a compiled config with a x1 or x2 grid, a launch mode
-(homogeneous grouped, heterogeneous grouped, expert-sorted offsets with empty groups, or a single
-GEMM), a tile schedule and, where the mode allows it, a K split, then shapes: K and N sometimes
-off the 8-element vector layout, M from 1 row up.  Operands are small random integers in
-[-2, 2], so every fp32 sum is exact and the expected output is the float64 product rounded once to
-the operand dtype: the launch must match it bit for bit (NaN-filled outputs also catch unwritten
-tiles).  The seeds are fixed; a failure names the seed and the drawn case.
+Each case draws a dtype (bf16, fp16, or fp32 with IEEE or TF32 products), a compiled config with a
+x1 or x2 grid, a launch mode (homogeneous grouped, heterogeneous grouped, expert-sorted offsets with
+empty groups, or a single GEMM), a tile schedule and, where the mode allows it, a K split (16-bit
+operands), then shapes: K and N sometimes off the 8-element vector layout, M from 1 row up.
+Operands are small random integers in [-2, 2], so every fp32 sum is exact and the expected output
+is the float64 product rounded once to the operand dtype (TF32 rounds such integers exactly): the
+launch must match it bit for bit (NaN-filled outputs also catch unwritten tiles).  The seeds are
+fixed; a failure names the seed and the drawn case.
 """
 
 from __future__ import annotations
@@ -48,7 +49,9 @@ def _draw_and_run(rng: random.Random, gen: torch.Generator) -> tuple[dict, list]
     def nan(shape, dtype):
         return torch.full(shape, float("nan"), device="cuda", dtype=dtype)
 
-    dtype = rng.choice([torch.bfloat16, torch.bfloat16, torch.float16])
+    dtype = rng.choice([torch.bfloat16, torch.bfloat16, torch.float16, torch.float32])
+    wide = dtype == torch.float32
+    precision = rng.choice(["ieee", "tf32"]) if wide else "ieee"
     base = rng.choice(config_pool(dtype))
     cfg = KernelConfig(base.block_m, base.block_n, base.block_k, base.group_size_m, base.num_warps, base.num_stages,
                        rng.choice([1, 1, 2]))
@@ -56,15 +59,16 @@ def _draw_and_run(rng: random.Random, gen: torch.Generator) -> tuple[dict, list]
     schedule = rng.choice(["static", "stealing"])
     k = dim(16, 2500, rng.choice([1, 8]))
     n = dim(8, 800, rng.choice([1, 8, 8]))
-    case = {"mode": mode, "dtype": str(dtype).split(".")[-1], "config": cfg.as_dict(), "schedule": schedule}
+    case = {"mode": mode, "dtype": str(dtype).split(".")[-1], "precision": precision, "config": cfg.as_dict(),
+            "schedule": schedule}
     if mode == "homogeneous":
         g, m = rng.randint(1, 24), rng.randint(1, 600)
-        split = rng.choice([1, 1, None, 2, 3]) if schedule == "static" else 1
+        split = rng.choice([1, 1, None, 2, 3]) if schedule == "static" and not wide else 1
         case.update(groups=g, m=m, k=k, n=n, split_k=split)
         a = [ints((m, k), dtype) for _ in range(g)]
         b = [ints((k, n), dtype) for _ in range(g)]
         c = [nan((m, n), dtype) for _ in range(g)]
-        launch_grouped(workspace_from_tensors(a, b, c, cfg), config=cfg, autotune=False, split_k=split,
+        launch_grouped(workspace_from_tensors(a, b, c, cfg), precision, config=cfg, autotune=False, split_k=split,
                        tile_schedule=schedule)
         torch.cuda.synchronize()
         return case, [e for e in range(g) if not torch.equal(c[e], expect(a[e], b[e], dtype))]
@@ -74,7 +78,7 @@ def _draw_and_run(rng: random.Random, gen: torch.Generator) -> tuple[dict, list]
         a = [ints((m, kk), dtype) for m, kk, _ in shapes]
         b = [ints((kk, nn), dtype) for _, kk, nn in shapes]
         c = [nan((m, nn), dtype) for m, _, nn in shapes]
-        launch_grouped(workspace_from_tensors(a, b, c, cfg), config=cfg, autotune=False, split_k=1,
+        launch_grouped(workspace_from_tensors(a, b, c, cfg), precision, config=cfg, autotune=False, split_k=1,
                        tile_schedule=schedule)
         torch.cuda.synchronize()
         return case, [e for e in range(len(shapes)) if not torch.equal(c[e], expect(a[e], b[e], dtype))]
@@ -87,7 +91,7 @@ def _draw_and_run(rng: random.Random, gen: torch.Generator) -> tuple[dict, list]
         a, b = ints((rows, k), dtype), ints((g, k, n), dtype)
         offs = torch.tensor(list(itertools.accumulate(sizes)), device="cuda", dtype=torch.int32)
         out = nan((rows, n), dtype)
-        grouped_mm(a, b, offs, out=out, config=cfg, autotune=False, tile_schedule=schedule)
+        grouped_mm(a, b, offs, out=out, config=cfg, input_precision=precision, autotune=False, tile_schedule=schedule)
         torch.cuda.synchronize()
         bad, start = [], 0
         for e, s in enumerate(sizes):
@@ -96,11 +100,11 @@ def _draw_and_run(rng: random.Random, gen: torch.Generator) -> tuple[dict, list]
             start += s
         return case, bad
     m = rng.randint(1, 1500)
-    split = rng.choice([1, None, 2, 4, 8])
+    split = rng.choice([1, None, 2, 4, 8]) if not wide else 1
     case.update(m=m, k=k, n=n, split_k=split)
     a, b = ints((m, k), dtype), ints((k, n), dtype)
     c = nan((m, n), dtype)
-    launch_matmul(a, b, c, cfg, autotune=False, split_k=split)
+    launch_matmul(a, b, c, cfg, precision, autotune=False, split_k=split)
     torch.cuda.synchronize()
     return case, [] if torch.equal(c, expect(a, b, dtype)) else [0]
 
