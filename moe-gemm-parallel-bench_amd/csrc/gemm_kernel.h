@@ -35,6 +35,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace moegemm {
 
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
@@ -839,9 +841,10 @@ grouped_gemm_kernel(KParams p) {
   // prefix chunk loaded above, so locating a tile needs no workgroup barrier.  A tile issues the
   // next unit's first K slices before its own last ones (FastTile::run_tile_chained,
   // PingPongTile::run_tile_chained), so the next unit must be known by then.  The static schedule
-  // knows it in advance.  Under work stealing (two-stage FastTiles only), lane 0 of wave 0 draws the
-  // ticket for the next unit once the tile's slice-1 copies are issued, and wave 0 resolves it at
-  // the tile's first slice boundary, before the barrier that publishes it to the workgroup.  Each
+  // knows it in advance.  Under work stealing (two-stage FastTiles and the ping-pong tile), lane 0 of
+  // wave 0 draws the ticket for the next unit and wave 0 resolves it before a barrier that publishes
+  // it to the workgroup: a two-stage tile draws once its slice-1 copies are issued and resolves at
+  // its first slice boundary, the ping-pong tile does both just before its prologue barrier.  Each
   // tile claims exactly its successor, as the unchained loop does, only earlier: a workgroup never
   // holds more than one unit ahead, so the last units of a queue still go to whichever workgroups
   // reach them first.  Every ticket is resolved within the tile that drew it, so none is
@@ -867,43 +870,59 @@ grouped_gemm_kernel(KParams p) {
         tm = uniform(tm);
         tn = uniform(tn);
       };
-      int ticket = -1;  // lane 0 of wave 0: drawn from queue tq.cur, not yet resolved
-      auto hooks = chain_hooks(
-          [&] {
-            if (stealing && threadIdx.x < 64) {
-              const int claimed = tq.claim(ticket);
-              if (threadIdx.x == 0) s_next[parity] = claimed;
-              ticket = -1;
-            }
-          },
-          [&](ProblemDesc& next, int& ntm, int& ntn) -> bool {
-            if (stealing) {
-              u = uniform(s_next[parity]);
-              parity ^= 1;
-            } else {
-              u += u_step;
-              if (u >= u_end) u = -1;
-            }
-            if (u < 0) return false;
-            describe(u, next, ntm, ntn);
-            return true;
-          },
-          [&] {
-            if (stealing && threadIdx.x == 0 && !((tq.drained >> tq.cur) & 1u))
-              ticket = atomicAdd(tq.q + tq.cur * kQueueStride, 1);
-          });
-      typename T::Chain ch;
-      ch.rot = 0;
-      ch.prefetched = false;
-      ProblemDesc pd, pdn;
-      int tm = 0, tn = 0, tmn = 0, tnn = 0;
-      if (stealing ? u >= 0 : u < u_end) {
-        describe(u, pd, tm, tn);
-        while (T::run_tile_chained(pd, tm, tn, smem, ch, hooks, pdn, tmn, tnn)) {
-          pd = pdn;
-          tm = tmn;
-          tn = tnn;
+      // The loop is compiled once per schedule, so the static one carries no queue code.
+      auto chain_loop = [&](auto steal) {
+        constexpr bool STEAL = decltype(steal)::value;
+        int ticket = -1;  // lane 0 of wave 0: drawn from queue tq.cur, not yet resolved
+        auto hooks = chain_hooks(
+            [&] {
+              if constexpr (STEAL) {
+                if (threadIdx.x < 64) {
+                  const int claimed = tq.claim(ticket);
+                  if (threadIdx.x == 0) s_next[parity] = claimed;
+                  ticket = -1;
+                }
+              }
+            },
+            [&](ProblemDesc& next, int& ntm, int& ntn) -> bool {
+              if constexpr (STEAL) {
+                u = uniform(s_next[parity]);
+                parity ^= 1;
+              } else {
+                u += u_step;
+                if (u >= u_end) u = -1;
+              }
+              if (u < 0) return false;
+              describe(u, next, ntm, ntn);
+              return true;
+            },
+            [&] {
+              if constexpr (STEAL) {
+                if (threadIdx.x == 0 && !((tq.drained >> tq.cur) & 1u))
+                  ticket = atomicAdd(tq.q + tq.cur * kQueueStride, 1);
+              }
+            });
+        typename T::Chain ch;
+        ch.rot = 0;
+        ch.prefetched = false;
+        ProblemDesc pd, pdn;
+        int tm = 0, tn = 0, tmn = 0, tnn = 0;
+        if (STEAL ? u >= 0 : u < u_end) {
+          describe(u, pd, tm, tn);
+          while (T::run_tile_chained(pd, tm, tn, smem, ch, hooks, pdn, tmn, tnn)) {
+            pd = pdn;
+            tm = tmn;
+            tn = tnn;
+          }
         }
+      };
+      if constexpr (T::CHAIN_STEALING) {
+        if (stealing)
+          chain_loop(std::true_type{});
+        else
+          chain_loop(std::false_type{});
+      } else {
+        chain_loop(std::false_type{});  // the condition above excludes stealing for these tiles
       }
       count_out();
       return;

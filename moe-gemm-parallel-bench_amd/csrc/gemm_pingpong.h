@@ -133,11 +133,12 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
   // (end of the memory or compute phase of K step 2) needs the stores done.  The next tile's buffers
   // rotate by K slices.  Tiles of fewer than STAGES slices, the last tile, and C that is not
   // 16-byte aligned run the unchained epilogue (zero slices, wait for every copy).  The next unit
-  // is computed right after the prologue barrier: only the static schedule is served here.
+  // is known right after the prologue barrier: the static schedule computes it, and under work
+  // stealing wave 0 claims it just before that barrier (see chained_group).
   static constexpr bool CHAIN_OK = Base::STAGED_OK && (STAGES & (STAGES - 1)) == 0;
   static constexpr int CHAIN_MIN_SLICES = 1;
   static constexpr int CHAIN_MAX_SLICES = 1 << 30;
-  static constexpr bool CHAIN_STEALING = false;
+  static constexpr bool CHAIN_STEALING = true;
   static constexpr int CHAIN_STORES = Base::CHAIN_STORES;
   static_assert(!CHAIN_OK || 3 * XMIN + CHAIN_STORES < 64, "outstanding operations must fit the 6-bit vmcnt");
   static_assert(!CHAIN_OK || (Base::CH_ROWS > 0 && Base::WTM % Base::CH_ROWS == 0 &&
@@ -176,17 +177,24 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
 
     const bool pre = ch.prefetched;
     const int rot = pre ? ch.rot : 0;
+    // Under work stealing, wave 0 claims the workgroup's next unit here and the first barrier
+    // publishes it.  Reading the claim waits for every vector memory operation of wave 0
+    // (vmcnt(0)): at this point that is the tile's own first slices and the previous tile's C
+    // stores, which the first K steps wait for anyway, or on a workgroup's first tile nothing.
     if (pre) {
       // Issued by the previous tile: slices 0, 1, 2, then its CHAIN_STORES stores, then slice 3.
       wait_vmcnt<3 * XMIN + CHAIN_STORES>();
+      sched.started();
+      sched.before_barrier();
     } else {
+      sched.started();
+      sched.before_barrier();
 #pragma unroll
       for (int s = 0; s < STAGES; ++s) Base::issue_stage(d, s, s * BK);
       wait_vmcnt<(STAGES - 1) * XMIN>();
     }
     phase_barrier();
     if constexpr (second) phase_barrier();  // group 1 runs one barrier behind
-    sched.started();
     const bool has_next = sched.next(next, ntm, ntn);
     const int kt_count = (pd.k + BK - 1) / BK;
     const bool c16 = ((reinterpret_cast<uintptr_t>(pd.c) & 15) == 0) && (pd.scm & 7) == 0;
