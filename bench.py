@@ -519,6 +519,7 @@ def main(argv=None) -> int:
             "model": "deepseek-v3 expert shapes (H=7168, F=2048, E=256, topk=8, P=8)",
             "tokens_per_expert": 512, "global_batch": 32 * 512, "seq_len": None, "parallelism": "ep8 (one rank)",
             "kernel_config": headline["config"], "scheduler": headline["scheduler"],
+            "tile_schedule": headline["tile_schedule"],
         },
         "roofline": {
             "bound": "mfma", "achieved": headline["tflops"], "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
