@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define MOEGEMM_ABI_VERSION 7
+#define MOEGEMM_ABI_VERSION 8
 
 #define MOEGEMM_OK 0
 #define MOEGEMM_ERR_INVALID (-1)   /* bad shape, pointer, dtype or parameter (Python: ValueError) */
@@ -174,6 +174,41 @@ int moegemm_grouped_gemm_splitk(const int64_t* a_ptrs, const int64_t* b_ptrs, co
                                 int32_t group_size_m, int32_t num_warps, int32_t num_stages,
                                 int32_t splits, int32_t grid_size, int32_t vector_layout,
                                 void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Stream-K tail in one launch, for launches whose tile count leaves the last round of a persistent
+ * grid partly idle (T = R * grid_size + r tiles take R + 1 rounds for R + r / grid_size rounds of
+ * work).  Replaces the same reference launches as the split-K entry points above (G = 1:
+ * kernels/matmul.py:332-392, homogeneous: kernels/grouped_gemm.py:321-397, dispatched by
+ * launch_grouped, :618-760), whose programs each take whole tiles pid, pid + grid, ...
+ * (:346-353, :397).  The first T - tail_tiles output tiles run whole, on the static schedule; the
+ * K slices (block_k each) of the last tail_tiles tiles are cut into grid_size equal runs in tile
+ * order, one per workgroup.  A run that covers part of a tile writes its fp32 partial into
+ * `workspace`; the last piece of a tile to arrive sums the tile's partials in K order
+ * (deterministic), casts and stores C.  With tail_tiles = r every workgroup ends after R + r /
+ * grid_size tile times.  `workspace` (256-byte aligned, at least moegemm_streamk_workspace_bytes()
+ * bytes) holds the 256 KiB counter area of the split-K workspace (zero before the first call, left
+ * zero by every call; one workspace can serve split-K and stream-K calls alike) then grid_size +
+ * tail_tiles partial slots of block_m * block_n floats.  Calls that share a workspace must not
+ * overlap.  Requirements: fp16/bf16 in the vector layout, grid_size >= 1, 1 <= tail_tiles <=
+ * min(T, 65536), and runs of at least ceil(K / block_k) / 63 slices (no tile cut into more than 64
+ * pieces).  Results differ from the unsplit launch's only in the order of the fp32 sums.
+ */
+int moegemm_streamk_workspace_bytes(int32_t tail_tiles, int32_t grid_size, int32_t block_m, int32_t block_n,
+                                    int64_t* bytes);
+int moegemm_matmul_streamk(const void* a, const void* b, void* c, int32_t m, int32_t n, int32_t k,
+                           int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
+                           int64_t stride_cm, int64_t stride_cn, int32_t dtype, int32_t block_m,
+                           int32_t block_n, int32_t block_k, int32_t group_size_m, int32_t num_warps,
+                           int32_t num_stages, int32_t tail_tiles, int32_t grid_size, void* workspace,
+                           int64_t workspace_bytes, void* stream);
+/* Homogeneous grouped counterpart (equal contiguous problems, vector_layout must be 1). */
+int moegemm_grouped_gemm_streamk(const int64_t* a_ptrs, const int64_t* b_ptrs, const int64_t* c_ptrs,
+                                 int32_t problem_count, int32_t m, int32_t n, int32_t k, int32_t dtype,
+                                 int32_t block_m, int32_t block_n, int32_t block_k, int32_t group_size_m,
+                                 int32_t num_warps, int32_t num_stages, int32_t tail_tiles,
+                                 int32_t grid_size, int32_t vector_layout, void* workspace,
+                                 int64_t workspace_bytes, void* stream);
 
 /* 1 when compiled kernel `index` of `dtype` can run the SwiGLU epilogue, 0 when not, < 0 on a bad
  * index.  No counterpart in the reference (its Triton pools have no fused epilogue). */

@@ -74,7 +74,11 @@ int check_common(int dtype, int input_precision, int group_size_m, const KernelE
 
 int launch(const KernelEntry* e, KParams& p, int grid, bool vector_layout, void* stream) {
   LaunchFn fn = (vector_layout && e->launch_fast) ? e->launch_fast : e->launch_general;
-  if (p.splits > 1) {  // split-K units: the fast path's split kernel (the callers checked the layout)
+  if (p.sk_tiles > 0) {  // stream-K tail: the fast path's stream-K kernel (the callers checked the layout)
+    if (!vector_layout || !e->launch_fast_streamk)
+      return fail(MOEGEMM_ERR_INVALID, "stream-K needs fp16/bf16 operands in the vector layout");
+    fn = e->launch_fast_streamk;
+  } else if (p.splits > 1) {  // split-K units: the fast path's split kernel (the callers checked the layout)
     if (!vector_layout || !e->launch_fast_split)
       return fail(MOEGEMM_ERR_INVALID, "split-K needs fp16/bf16 operands in the vector layout");
     fn = e->launch_fast_split;
@@ -135,6 +139,46 @@ int setup_splits(KParams& p, int64_t tiles, int32_t k, int32_t splits, int32_t b
   p.splits = (int32_t)effective;
   p.k_chunk = (int32_t)chunk;
   p.split_polls = split_polls();
+  p.total_tiles = (int32_t)tiles;
+  return MOEGEMM_OK;
+}
+
+// Stream-K tail workspace: the split-K counter area, then grid + tail_tiles fp32 partial slots
+// (piece (run v, tail tile j) writes slot v + j; see streamk_units in gemm_kernel.h).
+int64_t streamk_bytes(int64_t tail_tiles, int64_t grid, int64_t block_m, int64_t block_n) {
+  return kSplitCounterBytes + (grid + tail_tiles) * block_m * block_n * 4;
+}
+
+// Checks a stream-K plan and fills the launch fields: total_tiles tiles, the last tail_tiles of
+// them cut into `grid` runs of K slices.  A tail tile is cut into at most ceil(KT / floor(I / W))
+// + 1 pieces (I = tail_tiles * KT slices over W = grid runs); at most 64 are allowed, as for
+// split-K, so every run holds at least about KT / 63 slices.
+int setup_streamk(KParams& p, int64_t tiles, int32_t k, int32_t tail_tiles, int32_t grid, int32_t block_m,
+                  int32_t block_n, int32_t block_k, void* workspace, int64_t workspace_bytes) {
+  if (grid <= 0) return fail(MOEGEMM_ERR_INVALID, "stream-K needs a positive persistent grid (got %d)", grid);
+  if (tail_tiles < 1 || tail_tiles > tiles)
+    return fail(MOEGEMM_ERR_INVALID, "stream-K tail of %d tiles is outside [1, %lld]", tail_tiles, (long long)tiles);
+  if (tail_tiles > kSplitMaxTiles)
+    return fail(MOEGEMM_ERR_INVALID, "stream-K supports tails of at most %lld tiles (got %d)",
+                (long long)kSplitMaxTiles, tail_tiles);
+  const int64_t kt = cdiv(k, block_k);
+  const int64_t per_run = (int64_t)tail_tiles * kt / grid;
+  if (per_run < 1 || cdiv(kt, per_run) + 1 > 64)
+    return fail(MOEGEMM_ERR_INVALID,
+                "stream-K tail too thin: %d tiles of %lld K slices over %d runs cut a tile into more than 64 pieces",
+                tail_tiles, (long long)kt, grid);
+  const int64_t need = streamk_bytes(tail_tiles, grid, block_m, block_n);
+  if (!workspace || workspace_bytes < need)
+    return fail(MOEGEMM_ERR_INVALID, "stream-K workspace of %lld bytes is smaller than the %lld needed",
+                (long long)workspace_bytes, (long long)need);
+  if (reinterpret_cast<uintptr_t>(workspace) & 255)
+    return fail(MOEGEMM_ERR_INVALID, "stream-K workspace must be 256-byte aligned");
+  p.counters = static_cast<int32_t*>(workspace);
+  p.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + kSplitCounterBytes);
+  p.splits = 1;
+  p.k_chunk = k;
+  p.split_polls = 0;
+  p.sk_tiles = tail_tiles;
   p.total_tiles = (int32_t)tiles;
   return MOEGEMM_OK;
 }
@@ -447,6 +491,85 @@ int moegemm_grouped_gemm_splitk(const int64_t* a_ptrs, const int64_t* b_ptrs, co
   const int64_t units = (int64_t)p.total_tiles * p.splits;
   const int grid = grid_size <= 0 || grid_size > units ? (int)units : grid_size;
   return launch(e, p, grid, true, stream);
+}
+
+int moegemm_streamk_workspace_bytes(int32_t tail_tiles, int32_t grid_size, int32_t block_m, int32_t block_n,
+                                    int64_t* bytes) {
+  if (tail_tiles < 0 || grid_size < 1 || block_m <= 0 || block_n <= 0 || !bytes)
+    return fail(MOEGEMM_ERR_INVALID, "stream-K workspace query needs tail_tiles >= 0, grid_size >= 1 and a tile shape");
+  *bytes = streamk_bytes(tail_tiles, grid_size, block_m, block_n);
+  return MOEGEMM_OK;
+}
+
+int moegemm_matmul_streamk(const void* a, const void* b, void* c, int32_t m, int32_t n, int32_t k, int64_t stride_am,
+                           int64_t stride_ak, int64_t stride_bk, int64_t stride_bn, int64_t stride_cm,
+                           int64_t stride_cn, int32_t dtype, int32_t block_m, int32_t block_n, int32_t block_k,
+                           int32_t group_size_m, int32_t num_warps, int32_t num_stages, int32_t tail_tiles,
+                           int32_t grid_size, void* workspace, int64_t workspace_bytes, void* stream) {
+  const KernelEntry* e = nullptr;
+  int rc = check_common(dtype, MOEGEMM_PRECISION_IEEE, group_size_m, &e, block_m, block_n, block_k, num_warps,
+                        num_stages);
+  if (rc != MOEGEMM_OK) return rc;
+  if (!a || !b || !c) return fail(MOEGEMM_ERR_INVALID, "matrix pointers must be non-null");
+  if (m <= 0 || n <= 0 || k <= 0) return fail(MOEGEMM_ERR_INVALID, "shape must be positive (m=%d n=%d k=%d)", m, n, k);
+  if (!vector_layout_ok(a, b, c, m, n, k, stride_am, stride_ak, stride_bk, stride_bn, stride_cm, stride_cn, dtype) ||
+      !e->launch_fast)
+    return fail(MOEGEMM_ERR_INVALID, "stream-K needs fp16/bf16 operands in the vector layout");
+  const int64_t tiles = cdiv(m, block_m) * cdiv(n, block_n);
+  if (tiles > INT32_MAX) return fail(MOEGEMM_ERR_INVALID, "tile count %lld exceeds int32", (long long)tiles);
+  KParams p;
+  std::memset(&p, 0, sizeof(p));
+  p.mode = MODE_SINGLE;
+  p.a = a;
+  p.b = b;
+  p.c = c;
+  p.M = m;
+  p.N = n;
+  p.K = k;
+  p.sam = stride_am;
+  p.sak = stride_ak;
+  p.sbk = stride_bk;
+  p.sbn = stride_bn;
+  p.scm = stride_cm;
+  p.scn = stride_cn;
+  p.G = 1;
+  p.group_m = group_size_m;
+  rc = setup_streamk(p, tiles, k, tail_tiles, grid_size, block_m, block_n, block_k, workspace, workspace_bytes);
+  if (rc != MOEGEMM_OK) return rc;
+  return launch(e, p, grid_size, true, stream);
+}
+
+int moegemm_grouped_gemm_streamk(const int64_t* a_ptrs, const int64_t* b_ptrs, const int64_t* c_ptrs,
+                                 int32_t problem_count, int32_t m, int32_t n, int32_t k, int32_t dtype,
+                                 int32_t block_m, int32_t block_n, int32_t block_k, int32_t group_size_m,
+                                 int32_t num_warps, int32_t num_stages, int32_t tail_tiles, int32_t grid_size,
+                                 int32_t vector_layout, void* workspace, int64_t workspace_bytes, void* stream) {
+  const KernelEntry* e = nullptr;
+  int rc = check_common(dtype, MOEGEMM_PRECISION_IEEE, group_size_m, &e, block_m, block_n, block_k, num_warps,
+                        num_stages);
+  if (rc != MOEGEMM_OK) return rc;
+  if (problem_count <= 0) return fail(MOEGEMM_ERR_INVALID, "problem_count must be positive (got %d)", problem_count);
+  if (!a_ptrs || !b_ptrs || !c_ptrs) return fail(MOEGEMM_ERR_INVALID, "pointer tables must be non-null");
+  if (m <= 0 || n <= 0 || k <= 0)
+    return fail(MOEGEMM_ERR_INVALID, "homogeneous shape must be positive (m=%d n=%d k=%d)", m, n, k);
+  if (!vector_layout || !e->launch_fast)
+    return fail(MOEGEMM_ERR_INVALID, "stream-K needs fp16/bf16 operands in the vector layout");
+  const int64_t tiles = (int64_t)problem_count * cdiv(m, block_m) * cdiv(n, block_n);
+  if (tiles > INT32_MAX) return fail(MOEGEMM_ERR_INVALID, "tile count %lld exceeds int32", (long long)tiles);
+  KParams p;
+  std::memset(&p, 0, sizeof(p));
+  p.mode = MODE_HOMOGENEOUS;
+  p.a_ptrs = a_ptrs;
+  p.b_ptrs = b_ptrs;
+  p.c_ptrs = c_ptrs;
+  p.G = problem_count;
+  p.M = m;
+  p.N = n;
+  p.K = k;
+  p.group_m = group_size_m;
+  rc = setup_streamk(p, tiles, k, tail_tiles, grid_size, block_m, block_n, block_k, workspace, workspace_bytes);
+  if (rc != MOEGEMM_OK) return rc;
+  return launch(e, p, grid_size, true, stream);
 }
 
 int moegemm_kernel_swiglu(int dtype, int index) {

@@ -27,8 +27,9 @@
 //    fn + FN/2 the same output columns' up values, so the epilogue forms silu(gate) * up from the
 //    fp32 accumulators in registers and stores F-wide rows.  Needs an even FN and F a multiple of 8
 //    (checked by the host).
-//  * Split-K units (KParams::splits > 1) end with split_store instead of the C store: the fp32
-//    partial tile goes to the caller's workspace with device-coherent (sc1) 16-byte stores, the
+//  * Split-K units (ProblemDesc::splits > 1: a K range of a split-K tile or a piece of a stream-K
+//    tail tile) end with split_store instead of the C store: the fp32 partial tile goes to slot
+//    slot0 + split of the caller's workspace with device-coherent (sc1) 16-byte stores, the
 //    workgroup waits for them to complete before one atomic increment of the tile's counter, and
 //    the unit that brings the counter to `splits` re-arms it (writes 0) and reads all partials of
 //    the tile with device-coherent loads, summing them in split order — the same order whichever
@@ -393,7 +394,7 @@ struct FastTile {
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the previous round's LDS reads are done
         for (int r = 0; r < count; ++r) {
           if (KEEP_OWN && g0 + r == pd.split) continue;
-          const u32x4_t rs = make_rsrc(pd.partials + ((int64_t)pd.tile * splits + g0 + r) * (BM * BN), kSlotBytes);
+          const u32x4_t rs = make_rsrc(pd.partials + ((int64_t)pd.slot0 + g0 + r) * (BM * BN), kSlotBytes);
           for (int i = 0; i < cn; ++i)
             dma_copy16_coherent(rs, (uint32_t)chunk_offset(c0 + i, wave), region_lds + (uint32_t)((r * per + i) * 1024));
         }
@@ -461,7 +462,7 @@ struct FastTile {
     __shared__ uint32_t s_work;  // bit s: reduce slice s; bit 31: reduce the whole tile
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int splits = pd.splits;
-    const auto mine = __builtin_amdgcn_make_buffer_rsrc(pd.partials + ((int64_t)pd.tile * splits + pd.split) * (BM * BN),
+    const auto mine = __builtin_amdgcn_make_buffer_rsrc(pd.partials + ((int64_t)pd.slot0 + pd.split) * (BM * BN),
                                                         (short)0, (int)(BM * BN * 4), (int)kBufferFlags);
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm)
@@ -594,15 +595,20 @@ struct FastTile {
     }
   }
 
-  // Stores the tile (C, the SwiGLU output, or, in the split-K kernel, split-K partials).  The
-  // wave's copies must have landed (the staged epilogue reuses its LDS slots).
-  template <bool SPLIT = false>
+  // Stores the tile (C, the SwiGLU output, or split-K partials; see Epilogue).  The wave's copies
+  // must have landed (the staged epilogue reuses its LDS slots).
+  template <int EPI = EPI_C>
   __device__ static __forceinline__ void store_tile(const acc_t (&acc)[FM][FN], const ProblemDesc& pd, int m0,
                                                     int n0, int wave_m, int wave_n, char* smem) {
     const int lane = threadIdx.x & 63;
-    if constexpr (SPLIT) {
+    if constexpr (EPI == EPI_SPLIT) {
       split_store(acc, pd, m0, n0, wave_m, wave_n, smem);
       return;
+    } else if constexpr (EPI == EPI_EITHER) {
+      if (pd.splits > 1) {  // a piece; a whole tile takes the regular epilogue below
+        split_store(acc, pd, m0, n0, wave_m, wave_n, smem);
+        return;
+      }
     }
     if constexpr (SWIGLU_OK) {
       if (pd.swiglu) {
@@ -659,8 +665,8 @@ struct FastTile {
 
   // `before_store` runs once every copy has landed, before the epilogue barrier and the C stores
   // (a global atomic issued there overlaps them instead of delaying the in-order copy waits).
-  // SPLIT: the unit is one K range of a split-K tile (split_store instead of the C epilogue).
-  template <bool SPLIT, class Hook>
+  // EPI: the unit's epilogue (Epilogue; EPI_SPLIT for one K range of a split-K tile).
+  template <int EPI, class Hook>
   __device__ static __forceinline__ void run_tile(const ProblemDesc& pd, int tm, int tn, char* smem, bool,
                                                   Hook&& before_store) {
     static_assert(KK % 2 == 0, "fragment double buffer alternates by K step");
@@ -725,7 +731,7 @@ struct FastTile {
     compiler_fence();
     __builtin_amdgcn_s_barrier();
     compiler_fence();
-    store_tile<SPLIT>(acc, pd, m0, n0, wave_m, wave_n, smem);
+    store_tile<EPI>(acc, pd, m0, n0, wave_m, wave_n, smem);
   }
 
   // Cross-tile chaining of the two-stage tiles.  A workgroup on the static schedule knows its next

@@ -85,6 +85,10 @@ struct KParams {
   // block (the layout is at kQueueStride); zero between launches (the last workgroup of a launch
   // re-arms them).
   int32_t* queue;
+  // Stream-K tail (the stream-K kernel, single and homogeneous modes; 0 = off): the first
+  // total_tiles - sk_tiles tiles run whole on the static schedule, the last sk_tiles tiles are
+  // cut into `grid` equal runs of K slices, one per workgroup (see streamk_units).
+  int32_t sk_tiles;
 };
 
 struct ProblemDesc {
@@ -101,8 +105,13 @@ struct ProblemDesc {
                        // may then wait for each other, up to this many polls, to share its reduction
   float* partials;
   int32_t* counters;
+  int32_t slot0;       // partial slot of the tile's unit 0; unit s writes slot slot0 + s
 };
 
+
+// Epilogue of a unit: the C store, the fp32 partial of a split-K unit (split_store), or either,
+// chosen per unit by its piece count (stream-K launches: whole tiles store C, pieces store partials).
+enum Epilogue : int { EPI_C = 0, EPI_SPLIT = 1, EPI_EITHER = 2 };
 
 // Wave-uniform copies: values derived from LDS (the generic-mode prefix search) are treated as
 // divergent by the compiler; reading lane 0 makes every descriptor scalar again, so table loads
@@ -137,6 +146,7 @@ __device__ __forceinline__ void make_uniform(ProblemDesc& pd) {
   pd.split_wait = uniform(pd.split_wait);
   pd.partials = uniform(pd.partials);
   pd.counters = uniform(pd.counters);
+  pd.slot0 = uniform(pd.slot0);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -512,11 +522,11 @@ struct GemmTile {
 
   // -------------------------------------------------------------------------------------------
   // `before_store` runs once the K loop is done, before the C stores (the work-stealing scheduler
-  // draws its next ticket there).  Split-K runs only on the LDS-DMA tiles: SPLIT is never set here.
-  template <bool SPLIT, class Hook>
+  // draws its next ticket there).  Split-K runs only on the LDS-DMA tiles: EPI is always EPI_C here.
+  template <int EPI, class Hook>
   __device__ static __forceinline__ void run_tile(const ProblemDesc& pd, int tm, int tn, char* smem, bool tf32,
                                                   Hook&& before_store) {
-    static_assert(!SPLIT, "the general kernel has no split-K epilogue");
+    static_assert(EPI == EPI_C, "the general kernel has no split-K epilogue");
     const int wave = threadIdx.x >> 6;
     const int wave_m = wave / WN, wave_n = wave % WN;
     const int m0 = tm * BM, n0 = tn * BN;
@@ -758,12 +768,94 @@ __device__ __forceinline__ void simple_tile(const KParams& p, int t, ProblemDesc
   }
 }
 
+// Stream-K tail of a single or homogeneous launch (KParams::sk_tiles > 0), the body of the stream-K
+// kernel.  A launch of T equal tiles on a grid of W workgroups takes ceil(T / W) rounds, so with
+// T = R W + r (0 < r < W) its last round leaves W - r workgroups idle: 448 tiles on 256 CUs cost
+// two rounds for 1.75 rounds of work.  Here the first T - sk_tiles tiles run whole on the static
+// XCD-aware schedule (sk_tiles = r makes that R rounds), and the K slices of the last sk_tiles
+// tiles, I = sk_tiles * KT of them, are cut into W runs of I / W consecutive slices (in tile
+// order), one per workgroup, so every workgroup ends after R + r / W tile times.  A run that
+// covers part of a tile computes that piece and stores it as an fp32 partial (split_store, the
+// protocol in which the last arrival reduces and nobody waits); a run that covers a whole tile
+// stores C directly.  Runs are numbered XCD-contiguously (run v on XCD v / (W / 8)) so the pieces
+// of one tile, and the panels of neighbouring tiles, are read by workgroups of one XCD.
+// Bookkeeping, all from integers: slice i of the tail belongs to run floor(((i + 1) W - 1) / I);
+// tile j's pieces are runs first(j) .. last(j) (the owners of its first and last slice), piece
+// s = v - first(j) is unit s of the tile, and its partial goes to slot v + j: distinct pieces
+// (v, j) have distinct sums v + j (both indices grow along the tail), and the pieces of one tile
+// take the consecutive slots first(j) + j .. last(j) + j.  The workspace holds W + sk_tiles slots.
+template <class T>
+__device__ __forceinline__ void streamk_units(const KParams& p, char* smem) {
+  const int grid = gridDim.x;
+  const int b = (int)blockIdx.x;
+  const int main_tiles = p.total_tiles - p.sk_tiles;
+  auto describe = [&](int t, ProblemDesc& pd, int& tm, int& tn) {
+    simple_tile<T>(p, t, pd, tm, tn);
+    pd.swiglu = 0;
+    pd.splits = 1;
+    pd.split = 0;
+    pd.tile = 0;
+    pd.slot0 = 0;
+    pd.split_wait = 0;  // single protocol: the last piece to arrive reduces, nobody waits
+    pd.partials = p.partials;
+    pd.counters = p.counters;
+  };
+  // Whole tiles: the static schedule of the unsplit kernel over the first main_tiles tiles.
+  int u = b, u_step = grid, u_end = main_tiles;
+  if ((grid & 7) == 0) {
+    const int xcd = b & 7, per = grid >> 3;
+    u = (int)((int64_t)xcd * main_tiles / 8) + (b >> 3);
+    u_step = per;
+    u_end = (int)((int64_t)(xcd + 1) * main_tiles / 8);
+  }
+  for (; u < u_end; u += u_step) {
+    ProblemDesc pd;
+    int tm, tn;
+    describe(u, pd, tm, tn);
+    make_uniform(pd);
+    T::template run_tile<EPI_EITHER>(pd, uniform(tm), uniform(tn), smem, false, [] {});
+  }
+  // The tail: run v covers slices [v I / W, (v + 1) I / W).
+  const int64_t kt = (p.K + T::BK - 1) / T::BK;
+  const int64_t iters = (int64_t)p.sk_tiles * kt;
+  const int v = (grid & 7) == 0 ? (b & 7) * (grid >> 3) + (b >> 3) : b;
+  int64_t it = (int64_t)v * iters / grid;
+  const int64_t end = (int64_t)(v + 1) * iters / grid;
+  while (it < end) {
+    const int j = (int)(it / kt);
+    const int64_t k0 = it - (int64_t)j * kt;
+    const int64_t k1 = min(kt, k0 + (end - it));
+    const int first = (int)((((int64_t)j * kt + 1) * grid - 1) / iters);
+    const int last = (int)((((int64_t)j + 1) * kt * grid - 1) / iters);
+    ProblemDesc pd;
+    int tm, tn;
+    describe(main_tiles + j, pd, tm, tn);
+    pd.splits = last - first + 1;
+    pd.split = v - first;
+    pd.slot0 = first + j;
+    pd.tile = j;  // the tile's arrival counter
+    const int kb = (int)(k0 * T::BK);
+    pd.a += (int64_t)kb * pd.sak * T::ES;
+    pd.b += (int64_t)kb * pd.sbk * T::ES;
+    pd.k = min((int)((k1 - k0) * T::BK), pd.k - kb);
+    make_uniform(pd);
+    T::template run_tile<EPI_EITHER>(pd, uniform(tm), uniform(tn), smem, false, [] {});
+    it += k1 - k0;
+  }
+}
+
 // SPLIT: the split-K kernel (units are K ranges of tiles, split_store epilogue).  It is a kernel of
 // its own so that the split epilogue's registers do not weigh on the unsplit kernel's loops.
-template <class T, bool SPLIT>
+// STREAMK (with SPLIT): the stream-K kernel, a kernel of its own for the same reason.
+template <class T, bool SPLIT, bool STREAMK = false>
 __global__ void __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WAVES_PER_EU)))
 grouped_gemm_kernel(KParams p) {
   __shared__ __attribute__((aligned(16))) char smem[T::LDS_BYTES];
+  if constexpr (STREAMK) {
+    static_assert(SPLIT, "stream-K pieces use the split-K epilogue");
+    streamk_units<T>(p, smem);
+    return;
+  }
   int* s_pref = reinterpret_cast<int*>(smem + T::PREFIX_OFFSET);
   int* s_tot = s_pref + T::PREFIX + 1;
 
@@ -863,6 +955,7 @@ grouped_gemm_kernel(KParams p) {
         pd.splits = 1;
         pd.split = 0;
         pd.tile = unit;
+        pd.slot0 = 0;
         pd.split_wait = 0;
         pd.partials = p.partials;
         pd.counters = p.counters;
@@ -961,6 +1054,7 @@ grouped_gemm_kernel(KParams p) {
     pd.splits = splits;
     pd.split = u / p.total_tiles;
     pd.tile = t;
+    pd.slot0 = t * splits;
     pd.split_wait = units <= grid ? p.split_polls : 0;
     pd.partials = p.partials;
     pd.counters = p.counters;
@@ -972,7 +1066,7 @@ grouped_gemm_kernel(KParams p) {
     }
     make_uniform(pd);
     int ticket = -1;  // the next unit's ticket: drawn before the C stores, resolved after the tile
-    T::template run_tile<SPLIT>(pd, uniform(tm), uniform(tn), smem, p.tf32 != 0, [&] {
+    T::template run_tile<SPLIT ? EPI_SPLIT : EPI_C>(pd, uniform(tm), uniform(tn), smem, p.tf32 != 0, [&] {
       if (stealing && threadIdx.x == 0 && !((tq.drained >> tq.cur) & 1u))
         ticket = atomicAdd(tq.q + tq.cur * kQueueStride, 1);
     });

@@ -52,17 +52,17 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
   static_assert(Base::IA % NW == 0 && Base::IB % NW == 0, "every wave issues the same number of copies");
   static_assert(STAGES >= 3, "group 1 needs at least one phase between issuing and publishing a slice");
 
-  template <bool SPLIT, class Hook>
+  template <int EPI, class Hook>
   __device__ static __forceinline__ void run_tile(const ProblemDesc& pd, int tm, int tn, char* smem, bool tf32,
                                                   Hook&& before_store) {
     // Each group runs a copy of the schedule compiled for it (no group tests inside the K loop).
     if (__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) >= NW / 2)
-      group_tile<SPLIT, true>(pd, tm, tn, smem, before_store);
+      group_tile<EPI, true>(pd, tm, tn, smem, before_store);
     else
-      group_tile<SPLIT, false>(pd, tm, tn, smem, before_store);
+      group_tile<EPI, false>(pd, tm, tn, smem, before_store);
   }
 
-  template <bool SPLIT, bool SECOND, class Hook>
+  template <int EPI, bool SECOND, class Hook>
   __device__ static __forceinline__ void group_tile(const ProblemDesc& pd, int tm, int tn, char* smem,
                                                     Hook&& before_store) {
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -109,14 +109,17 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
     // stage C in the wave's own LDS slots; then the hook, as in FastTile.
     wait_vmcnt<0>();
     before_store();
-    if constexpr (SPLIT) {
-      // The split epilogue has workgroup barriers of its own: align the groups first.
-      if constexpr (!second) phase_barrier();
-      Base::template store_tile<true>(acc, pd, m0, n0, wave_m, wave_n, smem);
-    } else {
-      Base::store_tile(acc, pd, m0, n0, wave_m, wave_n, smem);
-      if constexpr (!second) phase_barrier();
+    if constexpr (EPI != EPI_C) {
+      if (EPI == EPI_SPLIT || pd.splits > 1) {
+        // The split epilogue has workgroup barriers of its own: align the groups first.
+        if constexpr (!second) phase_barrier();
+        Base::template store_tile<EPI_SPLIT>(acc, pd, m0, n0, wave_m, wave_n, smem);
+        return;
+      }
     }
+    // Unsplit tiles, also the whole tiles of a stream-K tail.
+    Base::store_tile(acc, pd, m0, n0, wave_m, wave_n, smem);
+    if constexpr (!second) phase_barrier();
   }
 
   // Cross-tile chaining on the static schedule of single and homogeneous launches, and of offsets

@@ -23,11 +23,12 @@ struct KernelEntry {
   LaunchFn launch_fast;     // null when the dtype has no fast path
   LaunchFn launch_general;
   LaunchFn launch_fast_split;  // the fast path's split-K kernel (null without a fast path)
+  LaunchFn launch_fast_streamk;  // the fast path's stream-K kernel (null without a fast path)
 };
 
-template <class T, bool SPLIT = false>
+template <class T, bool SPLIT = false, bool STREAMK = false>
 hipError_t launch_tile(const KParams& p, int grid, hipStream_t stream) {
-  hipLaunchKernelGGL((grouped_gemm_kernel<T, SPLIT>), dim3(grid), dim3(T::NT), 0, stream, p);
+  hipLaunchKernelGGL((grouped_gemm_kernel<T, SPLIT, STREAMK>), dim3(grid), dim3(T::NT), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -53,20 +54,32 @@ struct GemmTileEntry : GemmTile<E, BM, BN, BK, WM, WN> {};
   template __global__ void grouped_gemm_kernel<MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S), false>(KParams); \
   template __global__ void grouped_gemm_kernel<MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S), true>(KParams);  \
   template __global__ void grouped_gemm_kernel<MOEGEMM_GEN(E, BM, BN, BK, WM, WN, S), false>(KParams);
+// The stream-K kernels live in translation units of their own (inst_*_sk.hip): compiled next to
+// the other kernels of a tile, their presence in the module changed the register allocation of
+// those kernels (18 of 54 moved, one from 8 to 72 bytes of scratch).  Each such unit instantiates
+// the kernel and its host launcher; the tables refer to the launchers through these declarations.
+#define MOEGEMM_INST16_SK(E, BM, BN, BK, WM, WN, S)                                                        \
+  template __global__ void grouped_gemm_kernel<MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S), true, true>(KParams); \
+  template hipError_t launch_tile<MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S), true, true>(const KParams&, int,   \
+                                                                                      hipStream_t);
+#define MOEGEMM_EXTERN16_SK(E, BM, BN, BK, WM, WN, S)                                                          \
+  extern template hipError_t launch_tile<MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S), true, true>(const KParams&, int, \
+                                                                                             hipStream_t);
 #define MOEGEMM_ENTRY16(E, BM, BN, BK, WM, WN, S)                                             \
   KernelEntry{E::dtype, BM, BN, BK, (WM) * (WN), S, WM, WN,                                   \
               MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S)::LDS_BYTES,                              \
               MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S)::SWIGLU_OK ? 1 : 0,                      \
               &launch_tile<MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S)>,                          \
               &launch_tile<MOEGEMM_GEN(E, BM, BN, BK, WM, WN, S)>,                           \
-              &launch_tile<MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S), true>},
+              &launch_tile<MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S), true>,                    \
+              &launch_tile<MOEGEMM_FAST(E, BM, BN, BK, WM, WN, S), true, true>},
 
 #define MOEGEMM_INST32(E, BM, BN, BK, WM, WN, S) \
   template __global__ void grouped_gemm_kernel<MOEGEMM_GEN(E, BM, BN, BK, WM, WN, S), false>(KParams);
 #define MOEGEMM_ENTRY32(E, BM, BN, BK, WM, WN, S)                                             \
   KernelEntry{E::dtype, BM, BN, BK, (WM) * (WN), S, WM, WN,                                   \
               MOEGEMM_GEN(E, BM, BN, BK, WM, WN, S)::LDS_BYTES, 0, nullptr,                      \
-              &launch_tile<MOEGEMM_GEN(E, BM, BN, BK, WM, WN, S)>, nullptr},
+              &launch_tile<MOEGEMM_GEN(E, BM, BN, BK, WM, WN, S)>, nullptr, nullptr},
 
 // 16-bit menu (bf16 and f16 share it): large-M MFMA-bound tiles down to skinny-M streaming tiles.
 // STAGES is sized to the 160 KiB LDS of a CU; the 2-stage narrow tiles at the end fit two

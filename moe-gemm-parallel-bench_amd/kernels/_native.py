@@ -15,7 +15,7 @@ from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().with_name("libmoegemm.so")
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 OK = 0
 ERR_INVALID = -1
 ERR_NO_KERNEL = -2
@@ -67,6 +67,17 @@ SIGNATURES = {
          _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
     ),
     "moegemm_grouped_gemm_splitk": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+         _i32, _i32, _i32, _vp, _i64, _vp],
+    ),
+    "moegemm_streamk_workspace_bytes": (ctypes.c_int, [_i32, _i32, _i32, _i32, ctypes.POINTER(_i64)]),
+    "moegemm_matmul_streamk": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i32,
+         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _vp],
+    ),
+    "moegemm_grouped_gemm_streamk": (
         ctypes.c_int,
         [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
          _i32, _i32, _i32, _vp, _i64, _vp],
@@ -174,6 +185,29 @@ def splitk_workspace_bytes(tiles: int, splits: int, block_m: int, block_n: int) 
     return int(out.value)
 
 
+def streamk_workspace_bytes(tail_tiles: int, grid: int, block_m: int, block_n: int) -> int:
+    out = _i64(0)
+    check(library().moegemm_streamk_workspace_bytes(tail_tiles, grid, block_m, block_n, ctypes.byref(out)))
+    return int(out.value)
+
+
+def streamk_tail(tiles: int, grid: int, k: int, block_k: int) -> int:
+    """Tail tiles of a stream-K launch (0 when stream-K does not apply): the remainder r of
+    ``tiles`` over a ``grid`` of workgroups, so the whole tiles fill exact rounds and the r tail
+    tiles are spread over every workgroup.  0 when there is no remainder, or when the tail is too
+    thin for the library's limit of 64 pieces per tile."""
+    if tiles <= 0 or grid <= 0:
+        return 0
+    tail = tiles % grid
+    if tail == 0:
+        return 0
+    kt = -(-k // block_k)
+    per_run = tail * kt // grid
+    if per_run < 1 or -(-kt // per_run) + 1 > 64:
+        return 0
+    return tail
+
+
 # Split-K workspaces, one per (device, stream).  A workspace is never released once handed out, so
 # a captured graph that recorded its address stays valid; a larger need allocates a new one.
 _SPLITK_WORKSPACES: dict[tuple[int, int], list] = {}
@@ -207,6 +241,9 @@ def splitk_workspace(device, stream_handle: int, nbytes: int):
 QUEUE_BYTES = 4352
 NOALLOC_SCRATCH_BYTES = 64 * 1024 * 1024 + 256 * 1024  # MOEGEMM_NOALLOC_SCRATCH_BYTES
 TILE_SCHEDULES = ("static", "stealing")
+# Schedules of homogeneous grouped launches: also "streamk" (whole tiles in exact rounds, then a
+# stream-K tail; fp16/bf16 vector layouts).
+GROUPED_SCHEDULES = TILE_SCHEDULES + ("streamk",)
 _TILE_QUEUES: dict[tuple[int, int], object] = {}
 
 

@@ -23,6 +23,7 @@ from dataclasses import dataclass
 from . import _native
 from .matmul import (
     KernelConfig,
+    last_matmul_schedule,
     last_matmul_split,
     splitk_count,
     with_split_options,
@@ -70,7 +71,9 @@ class GroupedWorkspace:
     h_strides: object = None
     swiglu_config: KernelConfig | None = None
     split_k: int = 1  # K splits of the most recent launch (1 = no split-K)
-    tile_schedule: str = "static"  # "static" or "stealing" (work-stealing tile queues) of the last launch
+    # Tile schedule of the last launch: "static", "stealing" (work-stealing tile queues) or "streamk"
+    # (whole tiles in exact rounds, then a stream-K tail).
+    tile_schedule: str = "static"
 
     @property
     def problem_count(self) -> int:
@@ -336,22 +339,54 @@ def _grouped_splits(workspace: GroupedWorkspace, cfg: KernelConfig, dtype_code: 
     return splitk_count(workspace.tile_count_for(cfg), workspace.max_k, cfg.block_k, workspace.sm_count)
 
 
-def with_schedule_options(options, tile_schedule: str | None) -> list:
-    """(config, split, schedule) tuning candidates: unsplit options run under both schedules
-    unless ``tile_schedule`` pins one; split options stay static."""
+def with_schedule_options(options, tile_schedule: str | None, streamk_ok=None) -> list:
+    """(config, split, schedule) tuning candidates: unsplit options run under the static and the
+    stealing schedule, and under "streamk" where ``streamk_ok(config)`` says a stream-K tail
+    applies, unless ``tile_schedule`` pins one; split options stay static."""
     out = []
     for cfg, split in options:
+        streamk = split == 1 and streamk_ok is not None and streamk_ok(cfg)
         if split == 1 and tile_schedule is None:
             out += [(cfg, 1, "static"), (cfg, 1, "stealing")]
+            if streamk:
+                out.append((cfg, 1, "streamk"))
+        elif tile_schedule == "streamk":
+            if streamk:
+                out.append((cfg, 1, "streamk"))
         elif split == 1 or tile_schedule != "stealing":
             out.append((cfg, split, tile_schedule or "static"))
     return out
+
+
+def streamk_tail_for(workspace: GroupedWorkspace, cfg: KernelConfig, dtype_code: int) -> int:
+    """Tail tiles of a stream-K launch of this workspace with ``cfg`` (0: stream-K does not apply).
+    Homogeneous fp16/bf16 vector-layout groups only, on a grid of one workgroup per CU."""
+    if not workspace.homogeneous or cfg.cta_multiplier != 1 or not _vector_layout(workspace, dtype_code):
+        return 0
+    return _native.streamk_tail(workspace.tile_count_for(cfg), workspace.sm_count, workspace.max_k, cfg.block_k)
 
 
 def _launch_grouped_fixed(workspace: GroupedWorkspace, cfg: KernelConfig, dtype_code: int, precision: int,
                           split_k=None, schedule: str = "static") -> int:
     """One launch; returns the K splits used.  ``schedule`` "stealing" draws the tiles from the
     work-stealing queues (unsplit launches only)."""
+    if schedule == "streamk":
+        tail = streamk_tail_for(workspace, cfg, dtype_code)
+        if tail:
+            m, k, n = workspace.shapes[0]
+            grid = workspace.sm_count
+            stream = _native.current_stream_handle(workspace.a[0].device)
+            scratch = _native.splitk_workspace(workspace.a[0].device, stream,
+                                               _native.streamk_workspace_bytes(tail, grid, cfg.block_m, cfg.block_n))
+            status = _native.library().moegemm_grouped_gemm_streamk(
+                workspace.a_ptrs.data_ptr(), workspace.b_ptrs.data_ptr(), workspace.c_ptrs.data_ptr(),
+                workspace.problem_count, m, n, k, dtype_code,
+                cfg.block_m, cfg.block_n, cfg.block_k, cfg.group_size_m, cfg.num_warps, cfg.num_stages, tail, grid,
+                1, scratch.data_ptr(), scratch.numel(), stream,
+            )
+            _native.check(status)
+            return 1
+        schedule = "static"  # no partial last round: the static launch is the same work
     splits = _grouped_splits(workspace, cfg, dtype_code, split_k)
     if schedule == "stealing" and splits > 1:
         raise ValueError("the work-stealing schedule runs unsplit launches only (split_k must be 1)")
@@ -417,16 +452,19 @@ def launch_grouped(
     splits K inside the one launch when a homogeneous 16-bit group has too few tiles to fill the
     CUs; 1 disables it; n forces n.  ``workspace.split_k`` records what ran.
     ``tile_schedule`` (keyword-only, not in the reference's signature): "static" (tiles pid,
-    pid + grid, ... as the reference's programs take them) or "stealing" (per-XCD tile queues
-    with stealing); None lets the tuner measure both (static without autotuning).
-    ``workspace.tile_schedule`` records what ran.  G == 1 always runs the single GEMM.
+    pid + grid, ... as the reference's programs take them), "stealing" (per-XCD tile queues
+    with stealing) or "streamk" (whole tiles in exact rounds of one workgroup per CU, then the
+    remaining tiles' K slices spread over every workgroup; homogeneous 16-bit groups whose tile
+    count leaves a partial last round, static otherwise); None lets the tuner measure them
+    (static without autotuning).  ``workspace.tile_schedule`` records what ran.  G == 1 always
+    runs the single GEMM.
     """
     if split_k is not None and split_k < 1:
         raise ValueError("split_k must be None or a positive integer")
-    if tile_schedule is not None and tile_schedule not in _native.TILE_SCHEDULES:
-        raise ValueError(f"tile_schedule must be None or one of {_native.TILE_SCHEDULES}, got {tile_schedule!r}")
-    if tile_schedule == "stealing" and split_k is not None and split_k > 1:
-        raise ValueError("the work-stealing schedule runs unsplit launches only (split_k must be 1)")
+    if tile_schedule is not None and tile_schedule not in _native.GROUPED_SCHEDULES:
+        raise ValueError(f"tile_schedule must be None or one of {_native.GROUPED_SCHEDULES}, got {tile_schedule!r}")
+    if tile_schedule in ("stealing", "streamk") and split_k is not None and split_k > 1:
+        raise ValueError(f"the {tile_schedule} schedule runs unsplit launches only (split_k must be 1)")
     _require_runtime()
     cfg = config or workspace.config
     if workspace.problem_count == 1:
@@ -435,7 +473,7 @@ def launch_grouped(
         workspace.config = last_matmul_config(cfg) if autotune else cfg
         workspace.scheduler = "single_problem_matmul"
         workspace.split_k = last_matmul_split()
-        workspace.tile_schedule = "static"
+        workspace.tile_schedule = last_matmul_schedule()
         return
     dtype_code = _check_workspace(workspace)
     precision = _native.precision_code(input_precision, dtype_code)
@@ -453,17 +491,20 @@ def launch_grouped(
                 with_split_options(candidates, workspace.tile_count_for, workspace.max_k, workspace.sm_count,
                                    split_k, splittable),
                 tile_schedule,
+                lambda cfg: streamk_tail_for(workspace, cfg, dtype_code) > 0,
             )
             tuned = _tune(options, lambda o: _launch_grouped_fixed(workspace, o[0], dtype_code, precision, o[1], o[2]))
             _GROUPED_AUTOTUNE_CACHE[key] = tuned
         cfg, split_k, schedule = tuned
     else:
         schedule = tile_schedule or "static"
-        if schedule == "stealing" and split_k is None:
+        if schedule in ("stealing", "streamk") and split_k is None:
             split_k = 1
     workspace.split_k = _launch_grouped_fixed(workspace, cfg, dtype_code, precision, split_k, schedule)
     workspace.config = cfg
     workspace.scheduler = scheduler
+    if schedule == "streamk" and not streamk_tail_for(workspace, cfg, dtype_code):
+        schedule = "static"
     workspace.tile_schedule = schedule
 
 

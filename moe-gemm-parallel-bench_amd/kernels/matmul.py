@@ -318,11 +318,40 @@ def with_split_options(configs, tiles_of, k: int, sm_count: int, split_k, splitt
 
 
 _LAST_SPLIT: list[int] = [1]
+_LAST_SCHEDULE: list[str] = ["static"]
+STREAMK = "streamk"  # split option of a tuning candidate: whole tiles in exact rounds, then a stream-K tail
 
 
 def last_matmul_split() -> int:
     """K splits used by the most recent ``launch_matmul`` call (1 = no split-K)."""
     return _LAST_SPLIT[0]
+
+
+def last_matmul_schedule() -> str:
+    """Tile schedule of the most recent ``launch_matmul`` call: "static" or "streamk"."""
+    return _LAST_SCHEDULE[0]
+
+
+def _streamk_tail(a, b, c, m, n, k, cfg: KernelConfig) -> int:
+    """Tail tiles of a stream-K launch of this GEMM on one workgroup per CU (0: not applicable)."""
+    if not _vector_ok(a, b, c):
+        return 0
+    tiles = -(-m // cfg.block_m) * -(-n // cfg.block_n)
+    return _native.streamk_tail(tiles, _device_signature(a.device) % 1000, k, cfg.block_k)
+
+
+def _launch_fixed_streamk(a, b, c, m, n, k, cfg: KernelConfig, dtype_code: int, tail: int) -> None:
+    grid = _device_signature(a.device) % 1000
+    stream = _native.current_stream_handle(a.device)
+    workspace = _native.splitk_workspace(a.device, stream,
+                                         _native.streamk_workspace_bytes(tail, grid, cfg.block_m, cfg.block_n))
+    status = _native.library().moegemm_matmul_streamk(
+        a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k,
+        a.stride(0), a.stride(1), b.stride(0), b.stride(1), c.stride(0), c.stride(1), dtype_code,
+        cfg.block_m, cfg.block_n, cfg.block_k, cfg.group_size_m, cfg.num_warps, cfg.num_stages, tail, grid,
+        workspace.data_ptr(), workspace.numel(), stream,
+    )
+    _native.check(status)
 
 
 def _launch_fixed_splitk(a, b, c, m, n, k, cfg: KernelConfig, dtype_code: int, splits: int) -> None:
@@ -340,7 +369,16 @@ def _launch_fixed_splitk(a, b, c, m, n, k, cfg: KernelConfig, dtype_code: int, s
 
 
 def _launch_fixed(a, b, c, m, n, k, cfg: KernelConfig, dtype_code: int, precision: int, split_k=None) -> int:
-    """One launch; returns the K splits used (``split_k`` None = ``splitk_count``'s choice)."""
+    """One launch; returns the K splits used (``split_k`` None = ``splitk_count``'s choice,
+    ``STREAMK`` = a stream-K tail where one applies, else the unsplit launch)."""
+    _LAST_SCHEDULE[0] = "static"
+    if split_k == STREAMK:
+        tail = _streamk_tail(a, b, c, m, n, k, cfg) if precision == _native.PRECISION_IEEE else 0
+        if tail:
+            _launch_fixed_streamk(a, b, c, m, n, k, cfg, dtype_code, tail)
+            _LAST_SCHEDULE[0] = STREAMK
+            return 1
+        split_k = 1
     splits = 1
     if _vector_ok(a, b, c):
         tiles = -(-m // cfg.block_m) * -(-n // cfg.block_n)
@@ -395,9 +433,11 @@ def launch_matmul(
     if best is None:
         sm_count = _device_signature(a.device) % 1000
         configs = matmul_candidate_configs(m, n, k, dtype=a.dtype, sm_count=sm_count)
-        best = _tune(with_split_options(configs, lambda cfg: -(-m // cfg.block_m) * -(-n // cfg.block_n), k,
-                                        sm_count, split_k, _vector_ok(a, b, c)),
-                     lambda cand: _launch_fixed(a, b, c, m, n, k, cand[0], dtype_code, precision, cand[1]))
+        options = with_split_options(configs, lambda cfg: -(-m // cfg.block_m) * -(-n // cfg.block_n), k,
+                                     sm_count, split_k, _vector_ok(a, b, c))
+        if split_k is None:  # a stream-K tail where the tiles leave a partial last round
+            options += [(cfg, STREAMK) for cfg in configs if _streamk_tail(a, b, c, m, n, k, cfg)]
+        best = _tune(options, lambda cand: _launch_fixed(a, b, c, m, n, k, cand[0], dtype_code, precision, cand[1]))
         _AUTOTUNE_CACHE[key] = best
     _LAST_AUTOTUNED[0] = best[0]
     _LAST_SPLIT[0] = _launch_fixed(a, b, c, m, n, k, best[0], dtype_code, precision, best[1])
