@@ -11,6 +11,9 @@ Workloads (bf16, seeded inputs):
 * ``grouped``: DSV3 EP W13 at M_e=512, 32 x [512,7168]@[7168,4096] (the bench.py headline);
 * ``single``: one [16384,7168]@[7168,4096] GEMM with the same FLOPs, this project's kernel;
 * ``hipblaslt``: the same single GEMM through ``torch.mm`` (hipBLASLt on ROCm);
+* ``hipblaslt_batched``: the grouped workload itself through one ``torch.bmm`` on contiguous
+  [32, 512, 7168] and [32, 7168, 4096] operands (hipBLASLt's batched GEMM: the same 32 B matrices
+  and HBM bytes as ``grouped``);
 * ``decode``: DSV3 EP W13 at M_e=8, 32 x [8,7168]@[7168,4096] (HBM-bound; its rate is reported in
   TFLOP/s like the others, and its bytes per launch are 2 B x 32 x (8*7168 + 7168*4096 + 8*4096)).
 
@@ -31,7 +34,7 @@ import torch
 from kernels.grouped_gemm import build_grouped_workspace, launch_grouped
 from kernels.matmul import KernelConfig, launch_matmul
 
-WORKLOADS = ("grouped", "single", "hipblaslt", "decode")
+WORKLOADS = ("grouped", "single", "hipblaslt", "hipblaslt_batched", "decode")
 GROUPED_SHAPE = (512, 7168, 4096)  # (M_e, K, N) per expert
 DECODE_SHAPE = (8, 7168, 4096)
 EXPERTS = 32
@@ -147,6 +150,13 @@ def main(argv=None) -> int:
             steps["grouped"] = lambda: launch_grouped(ws)
         else:
             steps["grouped"] = lambda: launch_grouped(ws, config=pinned, autotune=False)
+    if "hipblaslt_batched" in workloads:
+        gen = torch.Generator(device="cuda").manual_seed(1234)
+        gm, gk, gn = GROUPED_SHAPE
+        a3 = (torch.randn(EXPERTS, gm, gk, device="cuda", generator=gen) * 0.1).to(dtype)
+        b3 = (torch.randn(EXPERTS, gk, gn, device="cuda", generator=gen) * 0.1).to(dtype)  # contiguous, not a view
+        c3 = torch.empty(EXPERTS, gm, gn, device="cuda", dtype=dtype)
+        steps["hipblaslt_batched"] = lambda: torch.bmm(a3, b3, out=c3)
     if "single" in workloads or "hipblaslt" in workloads:
         gen = torch.Generator(device="cuda").manual_seed(1234)
         a = (torch.randn(m, k, device="cuda", generator=gen) * 0.1).to(dtype)
