@@ -70,7 +70,8 @@ int moegemm_kernel_info(int dtype, int index, int32_t* out7);
  * grid (reference _grid_size, kernels/grouped_gemm.py:597-599); <= 0 means one workgroup per tile.
  * vector_layout != 0 promises that every problem is fp16/bf16 with unit inner strides, row
  * pitches and K, N multiples of 8 elements, C row pitch a multiple of 4, 16-byte aligned A/B and
- * 8-byte aligned C bases, and matrices under 2 GiB: the launch then uses the LDS-DMA kernel.
+ * 8-byte aligned C bases, A and C row pitches under 2^22 elements (256 rows under 2 GiB; any
+ * number of rows) and B under 2 GiB: the launch then uses the LDS-DMA kernel.
  * Otherwise (or for fp32) the general kernel runs, which accepts any strides and alignment.
  */
 int moegemm_grouped_gemm(const int64_t* a_ptrs, const int64_t* b_ptrs, const int64_t* c_ptrs,

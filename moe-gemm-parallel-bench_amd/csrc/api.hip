@@ -227,17 +227,27 @@ int device_scratch(void* stream, void** out) {
   return MOEGEMM_OK;
 }
 
+// Byte-range limits of the LDS-DMA kernels' 32-bit buffer offsets (see gemm_fast.h): A and C are
+// addressed through one resource per tile spanning at most kPanelRows rows, B through one
+// resource from the tile's first column to the end of the matrix.
+constexpr int64_t kTwoGiB = int64_t(1) << 31;
+constexpr int64_t kPanelRows = 256;  // the largest block_m of the menu
+
+bool panels_fit(int64_t k, int64_t sam, int64_t sbk, int64_t scm) {
+  return kPanelRows * sam * 2 < kTwoGiB && kPanelRows * scm * 2 < kTwoGiB && k * sbk * 2 < kTwoGiB;
+}
+
 // Preconditions of the LDS-DMA fast path for one problem (see gemm_fast.h).
 bool vector_layout_ok(const void* a, const void* b, const void* c, int64_t m, int64_t n, int64_t k, int64_t sam,
                       int64_t sak, int64_t sbk, int64_t sbn, int64_t scm, int64_t scn, int dtype) {
+  (void)m;  // A and C may be any number of rows: their resources are per tile
   if (dtype != DT_BF16 && dtype != DT_F16) return false;
   if (sak != 1 || sbn != 1 || scn != 1) return false;
   if (k % 8 || n % 8 || sam % 8 || sbk % 8 || scm % 4 || sam < k || sbk < n || scm < n) return false;
   if ((reinterpret_cast<uintptr_t>(a) & 15) || (reinterpret_cast<uintptr_t>(b) & 15) ||
       (reinterpret_cast<uintptr_t>(c) & 7))
     return false;
-  const int64_t limit = int64_t(1) << 31;
-  return (m * sam * 2 < limit) && (k * sbk * 2 < limit);
+  return panels_fit(k, sam, sbk, scm);
 }
 
 }  // namespace
@@ -632,13 +642,12 @@ static int offsets_impl(const void* a, const void* b, void* c, const int32_t* of
   p.total_tiles = (int32_t)tiles;
   p.swiglu = swiglu ? 1 : 0;
   const int grid = grid_size <= 0 ? p.total_tiles : (grid_size < p.total_tiles ? grid_size : p.total_tiles);
-  // Every group shares the strides, so one check covers all of them; the A resource of a tile spans
-  // at most block_m rows, each group's B resource one [k, n] panel.
+  // Every group shares the strides, so one check covers all of them; the A and C resources of a
+  // tile span at most block_m rows, each group's B resource one [k, n] panel.
   const bool vec = (dtype == DT_BF16 || dtype == DT_F16) && k % 8 == 0 && n % 8 == 0 && stride_am % 8 == 0 &&
                    stride_bk % 8 == 0 && stride_bg % 8 == 0 && stride_cm % 4 == 0 &&
                    (reinterpret_cast<uintptr_t>(a) & 15) == 0 && (reinterpret_cast<uintptr_t>(b) & 15) == 0 &&
-                   (reinterpret_cast<uintptr_t>(c) & 7) == 0 && (int64_t)block_m * stride_am * 2 < (int64_t(1) << 31) &&
-                   (int64_t)k * stride_bk * 2 < (int64_t(1) << 31);
+                   (reinterpret_cast<uintptr_t>(c) & 7) == 0 && panels_fit(k, stride_am, stride_bk, stride_cm);
   if (swiglu && !vec)
     return fail(MOEGEMM_ERR_INVALID, "the SwiGLU epilogue needs the vector layout (LDS-DMA kernel)");
   rc = set_queue(p, queue);

@@ -46,7 +46,10 @@
 //    row segments (8 rows x 128 bytes for a 64-column sub-tile).  The next tile's copies into
 //    those slots are issued by the same wave after its reads have returned.
 // Preconditions (checked by the host before choosing this variant): fp16/bf16, unit inner strides,
-// row pitches and the K, N extents multiples of 8 elements, every matrix < 2 GiB.
+// row pitches and the K, N extents multiples of 8 elements, 256 rows of A or C under 2 GiB (their
+// resources span one tile's rows, at most 256, and every byte offset in them stays below
+// kOutOfRange), and B under 2 GiB (its resource runs to the end of the matrix).  A and C may hold
+// any number of rows: each tile's resource base is a 64-bit address.
 #pragma once
 
 #include "gemm_kernel.h"

@@ -191,6 +191,17 @@ def streamk_workspace_bytes(tail_tiles: int, grid: int, block_m: int, block_n: i
     return int(out.value)
 
 
+PANEL_ROWS = 256  # the largest block_m of the menu
+_TWO_GIB = 1 << 31
+
+
+def panels_fit(k: int, sam: int, sbk: int, scm: int) -> bool:
+    """Byte-range limits of the LDS-DMA kernels' 32-bit buffer offsets, as the library checks them:
+    A and C are addressed through one resource per tile of at most PANEL_ROWS rows (any number of
+    rows in all), B through one resource running to the end of the [k, n] matrix."""
+    return PANEL_ROWS * sam * 2 < _TWO_GIB and PANEL_ROWS * scm * 2 < _TWO_GIB and k * sbk * 2 < _TWO_GIB
+
+
 def streamk_tail(tiles: int, grid: int, k: int, block_k: int) -> int:
     """Tail tiles of a stream-K launch (0 when stream-K does not apply): the remainder r of
     ``tiles`` over a ``grid`` of workgroups, so the whole tiles fill exact rounds and the r tail

@@ -290,12 +290,9 @@ def _grid_size(workspace: GroupedWorkspace, config: KernelConfig) -> int:
     return max(1, min(tiles, workspace.sm_count * config.cta_multiplier))
 
 
-_TWO_GIB = 1 << 31
-
-
 def _problem_vector_ok(a, b, c) -> bool:
     """Preconditions of the LDS-DMA kernel for one problem (see include/moegemm.h)."""
-    m, k = a.shape
+    k = a.shape[1]
     n = b.shape[1]
     sam, sak = a.stride()
     sbk, sbn = b.stride()
@@ -305,7 +302,7 @@ def _problem_vector_ok(a, b, c) -> bool:
         and k % 8 == 0 and n % 8 == 0 and sam % 8 == 0 and sbk % 8 == 0 and scm % 4 == 0
         and sam >= k and sbk >= n and scm >= n
         and a.data_ptr() % 16 == 0 and b.data_ptr() % 16 == 0 and c.data_ptr() % 8 == 0
-        and m * sam * 2 < _TWO_GIB and k * sbk * 2 < _TWO_GIB
+        and _native.panels_fit(k, sam, sbk, scm)
     )
 
 
@@ -522,7 +519,7 @@ def _swiglu_problem_ok(a, b, h) -> bool:
         and k % 8 == 0 and sam % 8 == 0 and sbk % 8 == 0 and shm % 4 == 0
         and sam >= k and sbk >= n and shm >= n // 2
         and a.data_ptr() % 16 == 0 and b.data_ptr() % 16 == 0 and h.data_ptr() % 8 == 0
-        and m * sam * 2 < _TWO_GIB and k * sbk * 2 < _TWO_GIB
+        and _native.panels_fit(k, sam, sbk, shm)
     )
 
 

@@ -269,16 +269,13 @@ def _require_runtime() -> None:
         raise RuntimeError(str(exc)) from exc
 
 
-_TWO_GIB = 1 << 31
-
-
 def _vector_ok(a, b, c) -> bool:
     """Preconditions of the LDS-DMA kernels for one 16-bit problem (see include/moegemm.h)."""
     import torch
 
     if a.dtype not in (torch.float16, torch.bfloat16):
         return False
-    m, k = a.shape
+    k = a.shape[1]
     n = b.shape[1]
     sam, sak = a.stride()
     sbk, sbn = b.stride()
@@ -288,7 +285,7 @@ def _vector_ok(a, b, c) -> bool:
         and k % 8 == 0 and n % 8 == 0 and sam % 8 == 0 and sbk % 8 == 0 and scm % 4 == 0
         and sam >= k and sbk >= n and scm >= n
         and a.data_ptr() % 16 == 0 and b.data_ptr() % 16 == 0 and c.data_ptr() % 8 == 0
-        and m * sam * 2 < _TWO_GIB and k * sbk * 2 < _TWO_GIB
+        and _native.panels_fit(k, sam, sbk, scm)
     )
 
 

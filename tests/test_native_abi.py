@@ -107,6 +107,28 @@ def test_matmul_entry_rejects_bad_arguments_without_launching():
     assert call(dtype=3) == _native.ERR_INVALID
 
 
+@pytest.mark.parametrize("m,sam,sbk,scm", [
+    (1 << 20, 4096, 64, 64),        # A of 8 GiB: any number of rows
+    (300, (1 << 22) - 8, 64, 64),   # the largest A pitch whose 256 rows stay under 2 GiB
+    (300, 1 << 22, 64, 64),
+    (300, 256, 64, (1 << 22) - 8),  # the same bound on C
+    (300, 256, 64, 1 << 22),
+    (300, 256, (1 << 22) - 8, 64),  # B [256, n] under 2 GiB
+    (300, 256, 1 << 22, 64),
+])
+def test_fast_layout_byte_limits_match_the_python_mirror(m, sam, sbk, scm):
+    """The split-K entry checks the LDS-DMA layout before its workspace, so a layout the library
+    accepts fails on the missing workspace instead, and neither reaches a launch."""
+    k, n = 256, 64
+    status = _native.library().moegemm_matmul_splitk(
+        4096, 8192, 12288, m, n, k, sam, 1, sbk, 1, scm, 1, _native.DTYPE_BF16, 256, 256, 32, 8, 8, 4, 2, 0,
+        None, 0, None)
+    assert status == _native.ERR_INVALID
+    accepted = "workspace" in _native.last_error()
+    assert accepted != ("vector layout" in _native.last_error())
+    assert accepted == _native.panels_fit(k, sam, sbk, scm)
+
+
 def test_status_mapping_to_python_exceptions():
     assert _grouped(dtype=9) == _native.ERR_INVALID
     with pytest.raises(ValueError):
