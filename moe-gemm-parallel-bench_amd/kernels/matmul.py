@@ -456,29 +456,46 @@ def _warm_clocks(launch, budget_ms: float = 100.0) -> None:
 
 
 _FINALISTS = 5
+# Rounds of the interleaved finalist timing.  One ~25 ms sample of a ~40 us launch spreads about
+# +-6 % on the MI355X (clock and power drift), against gaps of 2-5 % between the finalists of
+# mid-size launches (Mixtral W13 at M_e = 128); the median of seven rounds narrows the spread at
+# about 0.2 s per finalist.
+_FINAL_ROUNDS = 7
 
 
 def _tune(candidates, launch, prefer=None, prefer_margin: float = 0.03):
-    """Hot-time every candidate (graph replays, bounded) after a clock warm-up, then re-time the best
-    five interleaved (three rounds of A, B, C, D, E) and keep the lowest median, so a clock drift
-    during tuning shifts every finalist alike instead of favouring whichever ran at the better
-    moment, and a candidate that a noisy first pass ranked fourth or fifth still competes.
+    """Hot-time every candidate (graph replays, bounded) after a clock warm-up, twice (a forward and a
+    reverse sweep), then re-time the best five interleaved (seven rounds of A, B, C, D, E) and keep
+    the lowest median, so a clock drift during tuning shifts every finalist alike instead of
+    favouring whichever ran at the better moment, and a candidate that a noisy first pass ranked
+    fourth or fifth still competes.
 
     ``prefer`` (one of the candidates) always joins the finalists and is kept unless another
     finalist is faster by more than ``prefer_margin``: a choice already measured on the same
     workload is not overturned by timing noise."""
     candidates = list(candidates)
-    measured = []
+    first: dict[int, float] = {}
+    failed: set[int] = set()
     warmed = False
-    for cfg in candidates:
-        try:
-            if not warmed:
-                _warm_clocks(lambda cfg=cfg: launch(cfg))
-                warmed = True
-            median_ms = hot_autotune_bench(lambda cfg=cfg: launch(cfg), (0.5,))[0]
-        except (RuntimeError, ValueError):
-            continue
-        measured.append((median_ms, cfg))
+    # Two sweeps, forward then reverse, keeping each candidate's lower median: a candidate timed
+    # while the clock was still settling (the first ones after the warm-up) gets a second sample
+    # at the other end of the pass before the finalists are cut.
+    for order in (range(len(candidates)), reversed(range(len(candidates)))):
+        for index in order:
+            if index in failed:
+                continue
+            cfg = candidates[index]
+            try:
+                if not warmed:
+                    _warm_clocks(lambda cfg=cfg: launch(cfg))
+                    warmed = True
+                median_ms = hot_autotune_bench(lambda cfg=cfg: launch(cfg), (0.5,))[0]
+            except (RuntimeError, ValueError):
+                failed.add(index)
+                first.pop(index, None)
+                continue
+            first[index] = min(median_ms, first.get(index, math.inf))
+    measured = [(first[index], candidates[index]) for index in sorted(first)]
     if not measured:
         raise RuntimeError("every autotune candidate failed to launch")
     measured.sort(key=lambda item: item[0])
@@ -486,10 +503,10 @@ def _tune(candidates, launch, prefer=None, prefer_margin: float = 0.03):
     if prefer is not None and prefer not in finalists and any(cfg == prefer for _, cfg in measured):
         finalists.append(prefer)
     rounds: list[list[float]] = [[] for _ in finalists]
-    for _ in range(3):
+    for _ in range(_FINAL_ROUNDS):
         for index, cfg in enumerate(finalists):
             rounds[index].append(hot_autotune_bench(lambda cfg=cfg: launch(cfg), (0.5,))[0])
-    medians = [sorted(times)[1] for times in rounds]
+    medians = [sorted(times)[_FINAL_ROUNDS // 2] for times in rounds]
     best = finalists[medians.index(min(medians))]
     if prefer in finalists and medians[finalists.index(prefer)] <= min(medians) * (1.0 + prefer_margin):
         return prefer
