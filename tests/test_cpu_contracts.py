@@ -351,3 +351,53 @@ def test_tile_schedule_is_validated_before_touching_a_gpu():
     b = torch.zeros((2, 16, 8), dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="tile_schedule"):
         grouped_mm(a, b, torch.tensor([4, 8], dtype=torch.int32), tile_schedule="dynamic")
+
+
+def _fake_tuner_timing(monkeypatch, base_ms, first_penalty=None, failing=()):
+    """Replace the tuner's GPU timing with a deterministic model: each candidate's time is its
+    base, plus ``first_penalty`` on the very first timing after the clock warm-up; candidates in
+    ``failing`` raise as a launch the library rejects would."""
+    import kernels.matmul as mm
+
+    calls = []
+
+    def bench(fn, quantiles):
+        name = fn()
+        calls.append(name)
+        extra = first_penalty if first_penalty is not None and len(calls) == 1 else 0.0
+        return [base_ms[name] + extra for _ in quantiles]
+
+    def launch(cfg):
+        if cfg in failing:
+            raise RuntimeError(f"{cfg} rejected")
+        return cfg
+
+    monkeypatch.setattr(mm, "hot_autotune_bench", bench)
+    monkeypatch.setattr(mm, "_warm_clocks", lambda fn: fn())
+    return launch, calls
+
+
+def test_tuner_second_sweep_rescues_a_candidate_timed_while_the_clock_settled(monkeypatch):
+    from kernels.matmul import _FINAL_ROUNDS, _FINALISTS, _tune
+
+    base = {"best": 1.0, **{f"c{i}": 1.05 + 0.01 * i for i in range(8)}}
+    launch, calls = _fake_tuner_timing(monkeypatch, base, first_penalty=1.0)
+    candidates = ["best"] + [f"c{i}" for i in range(8)]
+    assert _tune(candidates, launch) == "best"
+    # Two sweeps over every candidate, then the finalists' interleaved rounds.
+    assert len(calls) == 2 * len(candidates) + _FINALISTS * _FINAL_ROUNDS
+    assert calls[:len(candidates)] == candidates and calls[len(candidates):2 * len(candidates)] == candidates[::-1]
+
+
+def test_tuner_skips_rejected_candidates_and_keeps_a_preferred_one_within_its_margin(monkeypatch):
+    from kernels.matmul import _tune
+
+    base = {"a": 1.00, "b": 1.02, "c": 0.90}
+    launch, _ = _fake_tuner_timing(monkeypatch, base, failing=("c",))
+    assert _tune(["a", "b", "c"], launch) == "a"
+    assert _tune(["a", "b", "c"], launch, prefer="b") == "b"  # 2 % slower: within the 3 % margin
+    launch, _ = _fake_tuner_timing(monkeypatch, {"a": 1.0, "b": 1.1})
+    assert _tune(["a", "b"], launch, prefer="b") == "a"
+    launch, _ = _fake_tuner_timing(monkeypatch, {"a": 1.0}, failing=("a",))
+    with pytest.raises(RuntimeError, match="every autotune candidate failed"):
+        _tune(["a"], launch)
