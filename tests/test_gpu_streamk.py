@@ -77,8 +77,10 @@ def _tiles16():
 
 @pytest.mark.parametrize("tile", _tiles16(), ids=lambda t: "x".join(map(str, t)))
 def test_every_tile_single_streamk_tail_exact(tile):
-    """A single GEMM with a K tail whose tile count leaves a partial last round on a grid of 24
-    (not a multiple of 8) and of 16: the tail tiles are cut into pieces across the runs."""
+    """A single GEMM with M, N and K tails, 15 tiles: on a grid of 4, three rounds of whole tiles
+    and a tail of 3, or a tail of all 15 (runs that hold whole tiles); on grids of 16 and 20 (20 is
+    not a multiple of 8, so runs are numbered without the XCD order) every tile is cut into pieces
+    across the runs."""
     bm, bn, bk, warps, stages = tile
     gen = torch.Generator(device="cuda").manual_seed(bm * 1000 + bn + bk)
     mt, nt = 3, 5
@@ -86,8 +88,8 @@ def test_every_tile_single_streamk_tail_exact(tile):
     a, b = _ints((m, k), gen, torch.bfloat16), _ints((k, n), gen, torch.bfloat16)
     exact = _exact(a, b, torch.bfloat16)
     tiles = mt * nt
-    for grid in (16, 24):
-        for tail in (tiles % grid or grid // 2, tiles):
+    for grid in (4, 16, 20):
+        for tail in sorted({tiles % grid or grid // 2, tiles}):
             if tail * ((k + bk - 1) // bk) < grid:
                 continue
             print(f"streamk single tile={tile} grid={grid} tail={tail} m={m} n={n} k={k}", flush=True)
@@ -112,7 +114,8 @@ def test_grouped_streamk_tails_exact(dtype):
         bm, bn, bk = tile[:3]
         tiles = g * -(-m // bm) * -(-n // bn)
         kt = -(-k // bk)
-        for grid, tail in ((8, tiles % 8 or 4), (32, tiles % 32 or 16), (8, tiles), (256, tiles)):
+        for grid, tail in ((8, tiles % 8 or 4), (20, tiles % 20 or 10), (32, tiles % 32 or 16), (8, tiles),
+                           (256, tiles)):
             per_run = tail * kt // grid
             if per_run < 1 or -(-kt // per_run) + 1 > 64:
                 continue  # a plan the library rejects (covered by test_library_rejects_bad_streamk_plans)
