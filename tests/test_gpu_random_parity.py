@@ -2,8 +2,8 @@
 
 Each case draws a dtype (bf16, fp16, or fp32 with IEEE or TF32 products), a compiled config with a
 x1 or x2 grid, a launch mode (homogeneous grouped, heterogeneous grouped, expert-sorted offsets with
-empty groups, or a single GEMM), a tile schedule and, where the mode allows it, a K split (16-bit
-operands), then shapes: K and N sometimes off the 8-element vector layout, M from 1 row up.
+empty groups, or a single GEMM), a tile schedule (static, work stealing, or for homogeneous 16-bit
+groups the stream-K tail) and, where the mode allows it, a K split (16-bit operands), then shapes: K and N sometimes off the 8-element vector layout, M from 1 row up.
 Operands are small random integers in [-2, 2], so every fp32 sum is exact and the expected output
 is the float64 product rounded once to the operand dtype (TF32 rounds such integers exactly): the
 launch must match it bit for bit (NaN-filled outputs also catch unwritten tiles).  The seeds are
@@ -56,7 +56,10 @@ def _draw_and_run(rng: random.Random, gen: torch.Generator) -> tuple[dict, list]
     cfg = KernelConfig(base.block_m, base.block_n, base.block_k, base.group_size_m, base.num_warps, base.num_stages,
                        rng.choice([1, 1, 2]))
     mode = rng.choice(["homogeneous", "homogeneous", "generic", "offsets", "offsets", "single"])
-    schedule = rng.choice(["static", "stealing"])
+    # Homogeneous 16-bit groups may also draw the stream-K tail (the launcher runs the static
+    # schedule where the tile count leaves no partial last round or the layout does not qualify).
+    streamk_ok = mode == "homogeneous" and not wide and cfg.cta_multiplier == 1
+    schedule = rng.choice(["static", "stealing", "streamk"] if streamk_ok else ["static", "stealing"])
     k = dim(16, 2500, rng.choice([1, 8]))
     n = dim(8, 800, rng.choice([1, 8, 8]))
     case = {"mode": mode, "dtype": str(dtype).split(".")[-1], "precision": precision, "config": cfg.as_dict(),
