@@ -166,7 +166,7 @@ def _case(projection: str, parallel_type: str, m: int, steps: int, warmup: int, 
         "tflops": tflops, "gbs": gbs, "bound": bound,
         "frac": tflops / PEAK_BF16_TFLOPS if bound == "mfma" else gbs / PEAK_HBM_GBS,
         "config": workspace.config.as_dict(), "scheduler": workspace.scheduler,
-        "tile_schedule": workspace.tile_schedule, "split_k": workspace.split_k,
+        "tile_schedule": workspace.tile_schedule, "split_k": workspace.split_k, "b_stream": workspace.b_stream,
         "normwise_error_sampled": error, "correct": bool(error <= (2e-3 if MODELS[model][4] == "fp16" else 1e-2)),
         "flops": flops, "ideal_bytes": nbytes,
     }
@@ -202,7 +202,8 @@ def _swiglu_case(m: int, steps: int, warmup: int, seed: int = 1234, settle_s: fl
         launch_gate_up_swiglu(workspace)
 
     def plain_step():
-        launch_grouped(workspace, config=cfg, autotune=False, split_k=1, tile_schedule="static")
+        launch_grouped(workspace, config=cfg, autotune=False, split_k=1, tile_schedule="static",
+                       b_stream=workspace.swiglu_b_stream)
 
     # SwiGLU and the plain W13 GEMM with the same tile, interleaved (three rounds each) after one
     # settle period, so the gap is measured under one clock state rather than against a case timed
@@ -220,7 +221,8 @@ def _swiglu_case(m: int, steps: int, warmup: int, seed: int = 1234, settle_s: fl
         "shape_mkn": list(workspace.shapes[0]), "ms": ms, "tflops": flops / (ms * 1e9),
         "gbs": nbytes / (ms * 1e6), "bound": "mfma", "frac": flops / (ms * 1e9) / PEAK_BF16_TFLOPS,
         "config": workspace.swiglu_config.as_dict(), "scheduler": workspace.scheduler,
-        "epilogue": "silu(gate)*up fused, H [M_e, F] stored", "plain_w13_ms_same_tile": plain_ms,
+        "b_stream": workspace.swiglu_b_stream, "epilogue": "silu(gate)*up fused, H [M_e, F] stored",
+        "plain_w13_ms_same_tile": plain_ms,
         "swiglu_over_plain": ms / plain_ms, "normwise_error_sampled": worst,
         "correct": bool(worst <= 1e-2), "flops": flops, "ideal_bytes": nbytes,
     }
@@ -236,7 +238,7 @@ def _ragged_case(steps: int, warmup: int, seed: int = 1234, settle_s: float = 0.
     import numpy as np
     import torch
 
-    from kernels.grouped_mm import build_offsets_workspace, grouped_mm, last_grouped_mm_config
+    from kernels.grouped_mm import build_offsets_workspace, grouped_mm, last_grouped_mm_b_stream, last_grouped_mm_config
     from utils.metrics import gemm_flops
 
     rng = np.random.default_rng(2024)
@@ -255,7 +257,8 @@ def _ragged_case(steps: int, warmup: int, seed: int = 1234, settle_s: float = 0.
             grouped_mm(ws.mat_a, ws.mat_b, ws.offs, out=ws.output, tile_schedule=schedule)
 
         step()  # autotune (untimed) for this schedule
-        steps_by_schedule[schedule] = (step, last_grouped_mm_config().as_dict())
+        steps_by_schedule[schedule] = (step, {**last_grouped_mm_config().as_dict(),
+                                              "b_stream": last_grouped_mm_b_stream()})
     # One settle period, then the schedules interleaved (three rounds each, median), so both see
     # the same clock state.
     _settle(steps_by_schedule["static"][0], settle_s)
@@ -519,7 +522,7 @@ def main(argv=None) -> int:
             "model": "deepseek-v3 expert shapes (H=7168, F=2048, E=256, topk=8, P=8)",
             "tokens_per_expert": 512, "global_batch": 32 * 512, "seq_len": None, "parallelism": "ep8 (one rank)",
             "kernel_config": headline["config"], "scheduler": headline["scheduler"],
-            "tile_schedule": headline["tile_schedule"],
+            "tile_schedule": headline["tile_schedule"], "b_stream": headline["b_stream"],
         },
         "roofline": {
             "bound": "mfma", "achieved": headline["tflops"], "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",

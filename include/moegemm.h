@@ -11,7 +11,12 @@
  *   - a call performs exactly one kernel launch on `stream` (or none for an empty problem set),
  *     never allocates, copies or synchronizes, and is therefore capturable in a HIP graph;
  *   - the return value is MOEGEMM_OK or a negative error code; moegemm_last_error() returns the
- *     message of the most recent failure on the calling thread.
+ *     message of the most recent failure on the calling thread;
+ *   - every launching call takes `b_stream` (0 or 1) just before `stream`: 1 issues the LDS-DMA
+ *     kernels' B copies as non-temporal loads (streamed, evicted first from the caches), 0 as
+ *     ordinary loads.  It changes no result, only speed, and which is faster depends on the
+ *     workload (it is a tuning choice, like the tile config; the general kernel ignores it).  It
+ *     has no counterpart in the reference's Triton launches, which take no cache policy.
  */
 #ifndef MOEGEMM_H
 #define MOEGEMM_H
@@ -22,7 +27,7 @@
 extern "C" {
 #endif
 
-#define MOEGEMM_ABI_VERSION 8
+#define MOEGEMM_ABI_VERSION 9
 
 #define MOEGEMM_OK 0
 #define MOEGEMM_ERR_INVALID (-1)   /* bad shape, pointer, dtype or parameter (Python: ValueError) */
@@ -79,7 +84,8 @@ int moegemm_grouped_gemm(const int64_t* a_ptrs, const int64_t* b_ptrs, const int
                          int32_t m, int32_t n, int32_t k, int32_t homogeneous, int32_t total_tiles,
                          int32_t dtype, int32_t input_precision, int32_t block_m, int32_t block_n,
                          int32_t block_k, int32_t group_size_m, int32_t num_warps,
-                         int32_t num_stages, int32_t grid_size, int32_t vector_layout, void* stream);
+                         int32_t num_stages, int32_t grid_size, int32_t vector_layout, int32_t b_stream,
+                         void* stream);
 
 /*
  * moegemm_grouped_gemm with a work-stealing tile scheduler instead of the static one: the
@@ -100,7 +106,7 @@ int moegemm_grouped_gemm_stealing(const int64_t* a_ptrs, const int64_t* b_ptrs,
                                   int32_t dtype, int32_t input_precision, int32_t block_m,
                                   int32_t block_n, int32_t block_k, int32_t group_size_m,
                                   int32_t num_warps, int32_t num_stages, int32_t grid_size,
-                                  int32_t vector_layout, void* queue, void* stream);
+                                  int32_t vector_layout, void* queue, int32_t b_stream, void* stream);
 
 /*
  * Packed Gate+Up projection with the SwiGLU activation fused into the epilogue: for each problem e
@@ -119,7 +125,7 @@ int moegemm_grouped_gemm_swiglu(const int64_t* a_ptrs, const int64_t* b_ptrs, co
                                 int32_t total_tiles, int32_t dtype, int32_t block_m,
                                 int32_t block_n, int32_t block_k, int32_t group_size_m,
                                 int32_t num_warps, int32_t num_stages, int32_t grid_size,
-                                int32_t vector_layout, void* stream);
+                                int32_t vector_layout, int32_t b_stream, void* stream);
 
 /*
  * Split-K in one launch, for problems with fewer output tiles than CUs (the reference's G = 1
@@ -143,7 +149,7 @@ int moegemm_matmul_splitk(const void* a, const void* b, void* c, int32_t m, int3
                           int64_t stride_bn, int64_t stride_cm, int64_t stride_cn, int32_t dtype,
                           int32_t block_m, int32_t block_n, int32_t block_k, int32_t group_size_m,
                           int32_t num_warps, int32_t num_stages, int32_t splits, int32_t grid_size,
-                          void* workspace, int64_t workspace_bytes, void* stream);
+                          void* workspace, int64_t workspace_bytes, int32_t b_stream, void* stream);
 /*
  * moegemm_matmul_splitk without the workspace argument: the partials and tile counters live in a
  * static device array of MOEGEMM_NOALLOC_SCRATCH_BYTES inside the library (one per GPU, held until
@@ -167,14 +173,14 @@ int moegemm_matmul_splitk_noalloc(const void* a, const void* b, void* c, int32_t
                                   int64_t stride_bn, int64_t stride_cm, int64_t stride_cn, int32_t dtype,
                                   int32_t block_m, int32_t block_n, int32_t block_k, int32_t group_size_m,
                                   int32_t num_warps, int32_t num_stages, int32_t splits, int32_t grid_size,
-                                  void* stream);
+                                  int32_t b_stream, void* stream);
 /* Homogeneous grouped counterpart (equal contiguous problems, vector_layout must be 1). */
 int moegemm_grouped_gemm_splitk(const int64_t* a_ptrs, const int64_t* b_ptrs, const int64_t* c_ptrs,
                                 int32_t problem_count, int32_t m, int32_t n, int32_t k,
                                 int32_t dtype, int32_t block_m, int32_t block_n, int32_t block_k,
                                 int32_t group_size_m, int32_t num_warps, int32_t num_stages,
                                 int32_t splits, int32_t grid_size, int32_t vector_layout,
-                                void* workspace, int64_t workspace_bytes, void* stream);
+                                void* workspace, int64_t workspace_bytes, int32_t b_stream, void* stream);
 
 /*
  * Stream-K tail in one launch, for launches whose tile count leaves the last round of a persistent
@@ -202,14 +208,14 @@ int moegemm_matmul_streamk(const void* a, const void* b, void* c, int32_t m, int
                            int64_t stride_cm, int64_t stride_cn, int32_t dtype, int32_t block_m,
                            int32_t block_n, int32_t block_k, int32_t group_size_m, int32_t num_warps,
                            int32_t num_stages, int32_t tail_tiles, int32_t grid_size, void* workspace,
-                           int64_t workspace_bytes, void* stream);
+                           int64_t workspace_bytes, int32_t b_stream, void* stream);
 /* Homogeneous grouped counterpart (equal contiguous problems, vector_layout must be 1). */
 int moegemm_grouped_gemm_streamk(const int64_t* a_ptrs, const int64_t* b_ptrs, const int64_t* c_ptrs,
                                  int32_t problem_count, int32_t m, int32_t n, int32_t k, int32_t dtype,
                                  int32_t block_m, int32_t block_n, int32_t block_k, int32_t group_size_m,
                                  int32_t num_warps, int32_t num_stages, int32_t tail_tiles,
                                  int32_t grid_size, int32_t vector_layout, void* workspace,
-                                 int64_t workspace_bytes, void* stream);
+                                 int64_t workspace_bytes, int32_t b_stream, void* stream);
 
 /* 1 when compiled kernel `index` of `dtype` can run the SwiGLU epilogue, 0 when not, < 0 on a bad
  * index.  No counterpart in the reference (its Triton pools have no fused epilogue). */
@@ -236,7 +242,7 @@ int moegemm_grouped_mm_offs(const void* a, const void* b, void* c, const int32_t
                             int64_t stride_cm, int32_t dtype, int32_t input_precision,
                             int32_t block_m, int32_t block_n, int32_t block_k,
                             int32_t group_size_m, int32_t num_warps, int32_t num_stages,
-                            int32_t grid_size, void* stream);
+                            int32_t grid_size, int32_t b_stream, void* stream);
 /*
  * Packed Gate+Up over the expert-sorted layout with the SwiGLU epilogue: B is [group_count, k, n]
  * with n = 2F columns [gate | up] per group (the packed W13 weights of reference
@@ -253,7 +259,7 @@ int moegemm_grouped_mm_offs_swiglu(const void* a, const void* b, void* h, const 
                                    int64_t stride_hm, int32_t dtype, int32_t block_m,
                                    int32_t block_n, int32_t block_k, int32_t group_size_m,
                                    int32_t num_warps, int32_t num_stages, int32_t grid_size,
-                                   void* stream);
+                                   int32_t b_stream, void* stream);
 /* The same launch with the work-stealing tile scheduler and queue of
  * moegemm_grouped_gemm_stealing; ragged offsets give tiles of unequal cost (partial M tiles). */
 int moegemm_grouped_mm_offs_stealing(const void* a, const void* b, void* c, const int32_t* offs,
@@ -263,7 +269,7 @@ int moegemm_grouped_mm_offs_stealing(const void* a, const void* b, void* c, cons
                                      int32_t block_m, int32_t block_n, int32_t block_k,
                                      int32_t group_size_m, int32_t num_warps,
                                      int32_t num_stages, int32_t grid_size, void* queue,
-                                     void* stream);
+                                     int32_t b_stream, void* stream);
 
 /*
  * Masked single GEMM with arbitrary strides, C = A @ B.  Replaces the Triton launch of
@@ -276,7 +282,7 @@ int moegemm_matmul(const void* a, const void* b, void* c, int32_t m, int32_t n, 
                    int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
                    int64_t stride_cm, int64_t stride_cn, int32_t dtype, int32_t input_precision,
                    int32_t block_m, int32_t block_n, int32_t block_k, int32_t group_size_m,
-                   int32_t num_warps, int32_t num_stages, int32_t grid_size, void* stream);
+                   int32_t num_warps, int32_t num_stages, int32_t grid_size, int32_t b_stream, void* stream);
 
 #ifdef __cplusplus
 }

@@ -72,7 +72,9 @@ int check_common(int dtype, int input_precision, int group_size_m, const KernelE
   return MOEGEMM_OK;
 }
 
-int launch(const KernelEntry* e, KParams& p, int grid, bool vector_layout, void* stream) {
+int launch(const KernelEntry* e, KParams& p, int grid, bool vector_layout, int32_t b_stream, void* stream) {
+  if (b_stream != 0 && b_stream != 1) return fail(MOEGEMM_ERR_INVALID, "b_stream must be 0 or 1 (got %d)", b_stream);
+  p.b_stream = b_stream;
   LaunchFn fn = (vector_layout && e->launch_fast) ? e->launch_fast : e->launch_general;
   if (p.sk_tiles > 0) {  // stream-K tail: the fast path's stream-K kernel (the callers checked the layout)
     if (!vector_layout || !e->launch_fast_streamk)
@@ -298,7 +300,7 @@ int grouped_impl(const int64_t* a_ptrs, const int64_t* b_ptrs, const int64_t* c_
                  const int64_t* strides, int32_t problem_count, int32_t m, int32_t n, int32_t k, int32_t homogeneous,
                  int32_t total_tiles, int32_t dtype, int32_t input_precision, int32_t block_m, int32_t block_n,
                  int32_t block_k, int32_t group_size_m, int32_t num_warps, int32_t num_stages, int32_t grid_size,
-                 int32_t vector_layout, bool swiglu, void* queue, void* stream) {
+                 int32_t vector_layout, bool swiglu, void* queue, int32_t b_stream, void* stream) {
   const KernelEntry* e = nullptr;
   int rc = check_common(dtype, input_precision, group_size_m, &e, block_m, block_n, block_k, num_warps, num_stages);
   if (rc != MOEGEMM_OK) return rc;
@@ -347,7 +349,7 @@ int grouped_impl(const int64_t* a_ptrs, const int64_t* b_ptrs, const int64_t* c_
   if (rc != MOEGEMM_OK) return rc;
   if (p.total_tiles == 0) return MOEGEMM_OK;
   int grid = grid_size <= 0 ? p.total_tiles : (grid_size < p.total_tiles ? grid_size : p.total_tiles);
-  return launch(e, p, grid, vector_layout != 0, stream);
+  return launch(e, p, grid, vector_layout != 0, b_stream, stream);
 }
 
 }  // namespace
@@ -358,10 +360,10 @@ int moegemm_grouped_gemm(const int64_t* a_ptrs, const int64_t* b_ptrs, const int
                          const int64_t* strides, int32_t problem_count, int32_t m, int32_t n, int32_t k,
                          int32_t homogeneous, int32_t total_tiles, int32_t dtype, int32_t input_precision,
                          int32_t block_m, int32_t block_n, int32_t block_k, int32_t group_size_m, int32_t num_warps,
-                         int32_t num_stages, int32_t grid_size, int32_t vector_layout, void* stream) {
+                         int32_t num_stages, int32_t grid_size, int32_t vector_layout, int32_t b_stream, void* stream) {
   return grouped_impl(a_ptrs, b_ptrs, c_ptrs, dims, strides, problem_count, m, n, k, homogeneous, total_tiles, dtype,
                       input_precision, block_m, block_n, block_k, group_size_m, num_warps, num_stages, grid_size,
-                      vector_layout, false, nullptr, stream);
+                      vector_layout, false, nullptr, b_stream, stream);
 }
 
 int moegemm_grouped_gemm_stealing(const int64_t* a_ptrs, const int64_t* b_ptrs, const int64_t* c_ptrs,
@@ -369,11 +371,11 @@ int moegemm_grouped_gemm_stealing(const int64_t* a_ptrs, const int64_t* b_ptrs, 
                                   int32_t n, int32_t k, int32_t homogeneous, int32_t total_tiles, int32_t dtype,
                                   int32_t input_precision, int32_t block_m, int32_t block_n, int32_t block_k,
                                   int32_t group_size_m, int32_t num_warps, int32_t num_stages, int32_t grid_size,
-                                  int32_t vector_layout, void* queue, void* stream) {
+                                  int32_t vector_layout, void* queue, int32_t b_stream, void* stream) {
   if (!queue) return fail(MOEGEMM_ERR_INVALID, "the work-stealing launch needs a tile queue");
   return grouped_impl(a_ptrs, b_ptrs, c_ptrs, dims, strides, problem_count, m, n, k, homogeneous, total_tiles, dtype,
                       input_precision, block_m, block_n, block_k, group_size_m, num_warps, num_stages, grid_size,
-                      vector_layout, false, queue, stream);
+                      vector_layout, false, queue, b_stream, stream);
 }
 
 int moegemm_grouped_gemm_swiglu(const int64_t* a_ptrs, const int64_t* b_ptrs, const int64_t* h_ptrs,
@@ -381,10 +383,10 @@ int moegemm_grouped_gemm_swiglu(const int64_t* a_ptrs, const int64_t* b_ptrs, co
                                 int32_t n, int32_t k, int32_t homogeneous, int32_t total_tiles, int32_t dtype,
                                 int32_t block_m, int32_t block_n, int32_t block_k, int32_t group_size_m,
                                 int32_t num_warps, int32_t num_stages, int32_t grid_size, int32_t vector_layout,
-                                void* stream) {
+                                int32_t b_stream, void* stream) {
   return grouped_impl(a_ptrs, b_ptrs, h_ptrs, dims, strides, problem_count, m, n, k, homogeneous, total_tiles, dtype,
                       MOEGEMM_PRECISION_IEEE, block_m, block_n, block_k, group_size_m, num_warps, num_stages,
-                      grid_size, vector_layout, true, nullptr, stream);
+                      grid_size, vector_layout, true, nullptr, b_stream, stream);
 }
 
 int moegemm_splitk_workspace_bytes(int32_t tiles, int32_t splits, int32_t block_m, int32_t block_n, int64_t* bytes) {
@@ -398,7 +400,7 @@ static int matmul_splitk_impl(const void* a, const void* b, void* c, int32_t m, 
                           int64_t stride_ak, int64_t stride_bk, int64_t stride_bn, int64_t stride_cm,
                           int64_t stride_cn, int32_t dtype, int32_t block_m, int32_t block_n, int32_t block_k,
                           int32_t group_size_m, int32_t num_warps, int32_t num_stages, int32_t splits,
-                          int32_t grid_size, void* workspace, int64_t workspace_bytes, void* stream) {
+                          int32_t grid_size, void* workspace, int64_t workspace_bytes, int32_t b_stream, void* stream) {
   const KernelEntry* e = nullptr;
   int rc = check_common(dtype, MOEGEMM_PRECISION_IEEE, group_size_m, &e, block_m, block_n, block_k, num_warps,
                         num_stages);
@@ -430,24 +432,25 @@ static int matmul_splitk_impl(const void* a, const void* b, void* c, int32_t m, 
   if (rc != MOEGEMM_OK) return rc;
   const int64_t units = (int64_t)p.total_tiles * p.splits;
   const int grid = grid_size <= 0 || grid_size > units ? (int)units : grid_size;
-  return launch(e, p, grid, true, stream);
+  return launch(e, p, grid, true, b_stream, stream);
 }
 
 int moegemm_matmul_splitk(const void* a, const void* b, void* c, int32_t m, int32_t n, int32_t k, int64_t stride_am,
                           int64_t stride_ak, int64_t stride_bk, int64_t stride_bn, int64_t stride_cm,
                           int64_t stride_cn, int32_t dtype, int32_t block_m, int32_t block_n, int32_t block_k,
                           int32_t group_size_m, int32_t num_warps, int32_t num_stages, int32_t splits,
-                          int32_t grid_size, void* workspace, int64_t workspace_bytes, void* stream) {
+                          int32_t grid_size, void* workspace, int64_t workspace_bytes, int32_t b_stream, void* stream) {
   return matmul_splitk_impl(a, b, c, m, n, k, stride_am, stride_ak, stride_bk, stride_bn, stride_cm, stride_cn, dtype,
                             block_m, block_n, block_k, group_size_m, num_warps, num_stages, splits, grid_size,
-                            workspace, workspace_bytes, stream);
+                            workspace, workspace_bytes, b_stream, stream);
 }
 
 int moegemm_matmul_splitk_noalloc(const void* a, const void* b, void* c, int32_t m, int32_t n, int32_t k,
                                   int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
                                   int64_t stride_cm, int64_t stride_cn, int32_t dtype, int32_t block_m,
                                   int32_t block_n, int32_t block_k, int32_t group_size_m, int32_t num_warps,
-                                  int32_t num_stages, int32_t splits, int32_t grid_size, void* stream) {
+                                  int32_t num_stages, int32_t splits, int32_t grid_size,
+                                  int32_t b_stream, void* stream) {
   // The split count that will run decides the bytes needed (split_plan, as setup_splits computes
   // it); a launch whose partials would not fit the static area is rejected before anything runs.
   // Other bad arguments are left to matmul_splitk_impl's checks.
@@ -466,14 +469,15 @@ int moegemm_matmul_splitk_noalloc(const void* a, const void* b, void* c, int32_t
   if (rc != MOEGEMM_OK) return rc;
   return matmul_splitk_impl(a, b, c, m, n, k, stride_am, stride_ak, stride_bk, stride_bn, stride_cm, stride_cn, dtype,
                             block_m, block_n, block_k, group_size_m, num_warps, num_stages, splits, grid_size, area,
-                            MOEGEMM_NOALLOC_SCRATCH_BYTES, stream);
+                            MOEGEMM_NOALLOC_SCRATCH_BYTES, b_stream, stream);
 }
 
 int moegemm_grouped_gemm_splitk(const int64_t* a_ptrs, const int64_t* b_ptrs, const int64_t* c_ptrs,
                                 int32_t problem_count, int32_t m, int32_t n, int32_t k, int32_t dtype,
                                 int32_t block_m, int32_t block_n, int32_t block_k, int32_t group_size_m,
                                 int32_t num_warps, int32_t num_stages, int32_t splits, int32_t grid_size,
-                                int32_t vector_layout, void* workspace, int64_t workspace_bytes, void* stream) {
+                                int32_t vector_layout, void* workspace, int64_t workspace_bytes,
+                                int32_t b_stream, void* stream) {
   const KernelEntry* e = nullptr;
   int rc = check_common(dtype, MOEGEMM_PRECISION_IEEE, group_size_m, &e, block_m, block_n, block_k, num_warps,
                         num_stages);
@@ -500,7 +504,7 @@ int moegemm_grouped_gemm_splitk(const int64_t* a_ptrs, const int64_t* b_ptrs, co
   if (rc != MOEGEMM_OK) return rc;
   const int64_t units = (int64_t)p.total_tiles * p.splits;
   const int grid = grid_size <= 0 || grid_size > units ? (int)units : grid_size;
-  return launch(e, p, grid, true, stream);
+  return launch(e, p, grid, true, b_stream, stream);
 }
 
 int moegemm_streamk_workspace_bytes(int32_t tail_tiles, int32_t grid_size, int32_t block_m, int32_t block_n,
@@ -515,7 +519,8 @@ int moegemm_matmul_streamk(const void* a, const void* b, void* c, int32_t m, int
                            int64_t stride_ak, int64_t stride_bk, int64_t stride_bn, int64_t stride_cm,
                            int64_t stride_cn, int32_t dtype, int32_t block_m, int32_t block_n, int32_t block_k,
                            int32_t group_size_m, int32_t num_warps, int32_t num_stages, int32_t tail_tiles,
-                           int32_t grid_size, void* workspace, int64_t workspace_bytes, void* stream) {
+                           int32_t grid_size, void* workspace, int64_t workspace_bytes,
+                           int32_t b_stream, void* stream) {
   const KernelEntry* e = nullptr;
   int rc = check_common(dtype, MOEGEMM_PRECISION_IEEE, group_size_m, &e, block_m, block_n, block_k, num_warps,
                         num_stages);
@@ -546,14 +551,15 @@ int moegemm_matmul_streamk(const void* a, const void* b, void* c, int32_t m, int
   p.group_m = group_size_m;
   rc = setup_streamk(p, tiles, k, tail_tiles, grid_size, block_m, block_n, block_k, workspace, workspace_bytes);
   if (rc != MOEGEMM_OK) return rc;
-  return launch(e, p, grid_size, true, stream);
+  return launch(e, p, grid_size, true, b_stream, stream);
 }
 
 int moegemm_grouped_gemm_streamk(const int64_t* a_ptrs, const int64_t* b_ptrs, const int64_t* c_ptrs,
                                  int32_t problem_count, int32_t m, int32_t n, int32_t k, int32_t dtype,
                                  int32_t block_m, int32_t block_n, int32_t block_k, int32_t group_size_m,
                                  int32_t num_warps, int32_t num_stages, int32_t tail_tiles, int32_t grid_size,
-                                 int32_t vector_layout, void* workspace, int64_t workspace_bytes, void* stream) {
+                                 int32_t vector_layout, void* workspace, int64_t workspace_bytes,
+                                 int32_t b_stream, void* stream) {
   const KernelEntry* e = nullptr;
   int rc = check_common(dtype, MOEGEMM_PRECISION_IEEE, group_size_m, &e, block_m, block_n, block_k, num_warps,
                         num_stages);
@@ -579,7 +585,7 @@ int moegemm_grouped_gemm_streamk(const int64_t* a_ptrs, const int64_t* b_ptrs, c
   p.group_m = group_size_m;
   rc = setup_streamk(p, tiles, k, tail_tiles, grid_size, block_m, block_n, block_k, workspace, workspace_bytes);
   if (rc != MOEGEMM_OK) return rc;
-  return launch(e, p, grid_size, true, stream);
+  return launch(e, p, grid_size, true, b_stream, stream);
 }
 
 int moegemm_kernel_swiglu(int dtype, int index) {
@@ -595,7 +601,7 @@ static int offsets_impl(const void* a, const void* b, void* c, const int32_t* of
                         int32_t n, int32_t k, int64_t stride_am, int64_t stride_bg, int64_t stride_bk,
                         int64_t stride_cm, int32_t dtype, int32_t input_precision, int32_t block_m, int32_t block_n,
                         int32_t block_k, int32_t group_size_m, int32_t num_warps, int32_t num_stages,
-                        int32_t grid_size, bool swiglu, void* queue, void* stream) {
+                        int32_t grid_size, bool swiglu, void* queue, int32_t b_stream, void* stream) {
   const KernelEntry* e = nullptr;
   int rc = check_common(dtype, input_precision, group_size_m, &e, block_m, block_n, block_k, num_warps, num_stages);
   if (rc != MOEGEMM_OK) return rc;
@@ -652,27 +658,27 @@ static int offsets_impl(const void* a, const void* b, void* c, const int32_t* of
     return fail(MOEGEMM_ERR_INVALID, "the SwiGLU epilogue needs the vector layout (LDS-DMA kernel)");
   rc = set_queue(p, queue);
   if (rc != MOEGEMM_OK) return rc;
-  return launch(e, p, grid, vec, stream);
+  return launch(e, p, grid, vec, b_stream, stream);
 }
 
 int moegemm_grouped_mm_offs(const void* a, const void* b, void* c, const int32_t* offs, int32_t group_count,
                             int32_t rows, int32_t n, int32_t k, int64_t stride_am, int64_t stride_bg,
                             int64_t stride_bk, int64_t stride_cm, int32_t dtype, int32_t input_precision,
                             int32_t block_m, int32_t block_n, int32_t block_k, int32_t group_size_m,
-                            int32_t num_warps, int32_t num_stages, int32_t grid_size, void* stream) {
+                            int32_t num_warps, int32_t num_stages, int32_t grid_size, int32_t b_stream, void* stream) {
   return offsets_impl(a, b, c, offs, group_count, rows, n, k, stride_am, stride_bg, stride_bk, stride_cm, dtype,
                       input_precision, block_m, block_n, block_k, group_size_m, num_warps, num_stages, grid_size,
-                      false, nullptr, stream);
+                      false, nullptr, b_stream, stream);
 }
 
 int moegemm_grouped_mm_offs_swiglu(const void* a, const void* b, void* h, const int32_t* offs, int32_t group_count,
                                    int32_t rows, int32_t n, int32_t k, int64_t stride_am, int64_t stride_bg,
                                    int64_t stride_bk, int64_t stride_hm, int32_t dtype, int32_t block_m,
                                    int32_t block_n, int32_t block_k, int32_t group_size_m, int32_t num_warps,
-                                   int32_t num_stages, int32_t grid_size, void* stream) {
+                                   int32_t num_stages, int32_t grid_size, int32_t b_stream, void* stream) {
   return offsets_impl(a, b, h, offs, group_count, rows, n, k, stride_am, stride_bg, stride_bk, stride_hm, dtype,
                       MOEGEMM_PRECISION_IEEE, block_m, block_n, block_k, group_size_m, num_warps, num_stages,
-                      grid_size, true, nullptr, stream);
+                      grid_size, true, nullptr, b_stream, stream);
 }
 
 int moegemm_grouped_mm_offs_stealing(const void* a, const void* b, void* c, const int32_t* offs,
@@ -680,17 +686,18 @@ int moegemm_grouped_mm_offs_stealing(const void* a, const void* b, void* c, cons
                                      int64_t stride_bg, int64_t stride_bk, int64_t stride_cm, int32_t dtype,
                                      int32_t input_precision, int32_t block_m, int32_t block_n, int32_t block_k,
                                      int32_t group_size_m, int32_t num_warps, int32_t num_stages,
-                                     int32_t grid_size, void* queue, void* stream) {
+                                     int32_t grid_size, void* queue, int32_t b_stream, void* stream) {
   if (!queue) return fail(MOEGEMM_ERR_INVALID, "the work-stealing launch needs a tile queue");
   return offsets_impl(a, b, c, offs, group_count, rows, n, k, stride_am, stride_bg, stride_bk, stride_cm, dtype,
                       input_precision, block_m, block_n, block_k, group_size_m, num_warps, num_stages, grid_size,
-                      false, queue, stream);
+                      false, queue, b_stream, stream);
 }
 
 int moegemm_matmul(const void* a, const void* b, void* c, int32_t m, int32_t n, int32_t k, int64_t stride_am,
                    int64_t stride_ak, int64_t stride_bk, int64_t stride_bn, int64_t stride_cm, int64_t stride_cn,
                    int32_t dtype, int32_t input_precision, int32_t block_m, int32_t block_n, int32_t block_k,
-                   int32_t group_size_m, int32_t num_warps, int32_t num_stages, int32_t grid_size, void* stream) {
+                   int32_t group_size_m, int32_t num_warps, int32_t num_stages, int32_t grid_size,
+                   int32_t b_stream, void* stream) {
   const KernelEntry* e = nullptr;
   int rc = check_common(dtype, input_precision, group_size_m, &e, block_m, block_n, block_k, num_warps, num_stages);
   if (rc != MOEGEMM_OK) return rc;
@@ -719,7 +726,7 @@ int moegemm_matmul(const void* a, const void* b, void* c, int32_t m, int32_t n, 
   p.total_tiles = (int32_t)tiles;
   int grid = grid_size <= 0 ? p.total_tiles : (grid_size < p.total_tiles ? grid_size : p.total_tiles);
   return launch(e, p, grid, vector_layout_ok(a, b, c, m, n, k, stride_am, stride_ak, stride_bk, stride_bn, stride_cm,
-                                           stride_cn, dtype), stream);
+                                           stride_cn, dtype), b_stream, stream);
 }
 
 }  // extern "C"

@@ -91,6 +91,17 @@ __device__ __forceinline__ void dma_copy16(u32x4_t rsrc, uint32_t voffset, uint3
 #pragma clang diagnostic pop
 }
 
+// dma_copy16 with a non-temporal (nt) read: streamed data, evicted first from the caches.
+__device__ __forceinline__ void dma_copy16_nt(u32x4_t rsrc, uint32_t voffset, uint32_t lds) {
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen nt lds"
+               :
+               : "v"(voffset), "s"(rsrc), "s"(lds)
+               : "memory", "m0");
+#pragma clang diagnostic pop
+}
+
 // dma_copy16 with device-coherent (sc1) reads: for data that other workgroups, possibly on other
 // XCDs, wrote with sc1 stores (the split-K partials).
 __device__ __forceinline__ void dma_copy16_coherent(u32x4_t rsrc, uint32_t voffset, uint32_t lds) {
@@ -170,6 +181,7 @@ struct FastTile {
     int32_t k;
     uint32_t ldb_bytes;
     uint32_t lds_wave;   // LDS byte address of this wave's first 1 KiB slot in stage 0
+    int32_t b_stream;    // B copies non-temporal (ProblemDesc::b_stream)
   };
 
   __device__ static __forceinline__ void setup_dma(Dma& d, const ProblemDesc& pd, int m0, int n0, const char* smem) {
@@ -177,6 +189,7 @@ struct FastTile {
     const uint32_t lda_bytes = (uint32_t)pd.sam * 2u;
     d.ldb_bytes = (uint32_t)pd.sbk * 2u;
     d.k = pd.k;
+    d.b_stream = pd.b_stream;
     const int rows = min(BM, pd.m - m0);
     d.ra = make_rsrc(pd.a + (int64_t)m0 * lda_bytes, (uint32_t)rows * lda_bytes);
     if (pd.swiglu)
@@ -227,12 +240,23 @@ struct FastTile {
       }
     }
     const uint32_t kstep = (uint32_t)k0 * d.ldb_bytes;
+    if (d.b_stream)
+      issue_b<true>(d, base, kstep, wave);
+    else
+      issue_b<false>(d, base, kstep, wave);
+  }
+
+  template <bool NT>
+  __device__ static __forceinline__ void issue_b(const Dma& d, uint32_t base, uint32_t kstep, int wave) {
 #pragma unroll
     for (int q = 0; q < QB; ++q) {
       const int j = wave + q * NW;
       if (IB % NW == 0 || j < IB) {
         const uint32_t off = d.b_off[q] == kOutOfRange ? kOutOfRange : d.b_off[q] + kstep;
-        dma_copy16(d.rb, off, base + (uint32_t)(A_BYTES + q * NW * 1024));
+        if constexpr (NT)
+          dma_copy16_nt(d.rb, off, base + (uint32_t)(A_BYTES + q * NW * 1024));
+        else
+          dma_copy16(d.rb, off, base + (uint32_t)(A_BYTES + q * NW * 1024));
       }
     }
   }

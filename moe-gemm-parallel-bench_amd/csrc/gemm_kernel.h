@@ -89,6 +89,9 @@ struct KParams {
   // total_tiles - sk_tiles tiles run whole on the static schedule, the last sk_tiles tiles are
   // cut into `grid` equal runs of K slices, one per workgroup (see streamk_units).
   int32_t sk_tiles;
+  // B copy policy of the LDS-DMA tiles: 1 issues B's global -> LDS copies non-temporal (streamed
+  // data, evicted first from the caches), 0 as ordinary loads.  A's copies are always ordinary.
+  int32_t b_stream;
 };
 
 struct ProblemDesc {
@@ -106,6 +109,7 @@ struct ProblemDesc {
   float* partials;
   int32_t* counters;
   int32_t slot0;       // partial slot of the tile's unit 0; unit s writes slot slot0 + s
+  int32_t b_stream;    // KParams::b_stream
 };
 
 
@@ -147,6 +151,7 @@ __device__ __forceinline__ void make_uniform(ProblemDesc& pd) {
   pd.partials = uniform(pd.partials);
   pd.counters = uniform(pd.counters);
   pd.slot0 = uniform(pd.slot0);
+  pd.b_stream = uniform(pd.b_stream);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -729,6 +734,7 @@ __device__ __forceinline__ void searched_tile(const KParams& p, const int* s_pre
     pd.b = reinterpret_cast<const char*>(p.b_ptrs[e]);
     pd.c = reinterpret_cast<char*>(p.c_ptrs[e]);
   }
+  pd.b_stream = p.b_stream;
   const int mt = (pd.m + T::BM - 1) / T::BM, nt = (pd.n + T::BN - 1) / T::BN;
   group_m_order(local, mt, nt, p.group_m, tm, tn);
 }
@@ -749,6 +755,7 @@ __device__ __forceinline__ ChainHooks<BeforeBarrier, Next, Started> chain_hooks(
 template <class T>
 __device__ __forceinline__ void simple_tile(const KParams& p, int t, ProblemDesc& pd, int& tm, int& tn) {
   const int mt = (p.M + T::BM - 1) / T::BM, nt = (p.N + T::BN - 1) / T::BN;
+  pd.b_stream = p.b_stream;
   if (p.mode == MODE_SINGLE) {
     pd.a = static_cast<const char*>(p.a);
     pd.b = static_cast<const char*>(p.b);

@@ -15,7 +15,7 @@ from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().with_name("libmoegemm.so")
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 OK = 0
 ERR_INVALID = -1
 ERR_NO_KERNEL = -2
@@ -42,65 +42,65 @@ SIGNATURES = {
     "moegemm_grouped_gemm": (
         ctypes.c_int,
         [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
-         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
+         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
     ),
     "moegemm_grouped_gemm_stealing": (
         ctypes.c_int,
         [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
-         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp],
+         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i32, _vp],
     ),
     "moegemm_grouped_gemm_swiglu": (
         ctypes.c_int,
         [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
-         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
+         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
     ),
     "moegemm_kernel_swiglu": (ctypes.c_int, [ctypes.c_int, ctypes.c_int]),
     "moegemm_splitk_workspace_bytes": (ctypes.c_int, [_i32, _i32, _i32, _i32, ctypes.POINTER(_i64)]),
     "moegemm_matmul_splitk": (
         ctypes.c_int,
         [_vp, _vp, _vp, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i32,
-         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _vp],
+         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i32, _vp],
     ),
     "moegemm_matmul_splitk_noalloc": (
         ctypes.c_int,
         [_vp, _vp, _vp, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i32,
-         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
+         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
     ),
     "moegemm_grouped_gemm_splitk": (
         ctypes.c_int,
         [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
-         _i32, _i32, _i32, _vp, _i64, _vp],
+         _i32, _i32, _i32, _vp, _i64, _i32, _vp],
     ),
     "moegemm_streamk_workspace_bytes": (ctypes.c_int, [_i32, _i32, _i32, _i32, ctypes.POINTER(_i64)]),
     "moegemm_matmul_streamk": (
         ctypes.c_int,
         [_vp, _vp, _vp, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i32,
-         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _vp],
+         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i32, _vp],
     ),
     "moegemm_grouped_gemm_streamk": (
         ctypes.c_int,
         [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
-         _i32, _i32, _i32, _vp, _i64, _vp],
+         _i32, _i32, _i32, _vp, _i64, _i32, _vp],
     ),
     "moegemm_grouped_mm_offs": (
         ctypes.c_int,
         [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i32, _i32,
-         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
+         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
     ),
     "moegemm_grouped_mm_offs_swiglu": (
         ctypes.c_int,
         [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i32,
-         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
+         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
     ),
     "moegemm_grouped_mm_offs_stealing": (
         ctypes.c_int,
         [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i32, _i32,
-         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp],
+         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i32, _vp],
     ),
     "moegemm_matmul": (
         ctypes.c_int,
         [_vp, _vp, _vp, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32,
-         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
+         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
     ),
 }
 

@@ -23,6 +23,7 @@ from dataclasses import dataclass
 from . import _native
 from .matmul import (
     KernelConfig,
+    last_matmul_b_stream,
     last_matmul_schedule,
     last_matmul_split,
     splitk_count,
@@ -74,6 +75,8 @@ class GroupedWorkspace:
     # Tile schedule of the last launch: "static", "stealing" (work-stealing tile queues) or "streamk"
     # (whole tiles in exact rounds, then a stream-K tail).
     tile_schedule: str = "static"
+    b_stream: int = 0  # 1: the last launch issued its B copies non-temporal
+    swiglu_b_stream: int = 0  # the same for the last launch_gate_up_swiglu call
 
     @property
     def problem_count(self) -> int:
@@ -364,9 +367,10 @@ def streamk_tail_for(workspace: GroupedWorkspace, cfg: KernelConfig, dtype_code:
 
 
 def _launch_grouped_fixed(workspace: GroupedWorkspace, cfg: KernelConfig, dtype_code: int, precision: int,
-                          split_k=None, schedule: str = "static") -> int:
+                          split_k=None, schedule: str = "static", b_stream: int = 0) -> int:
     """One launch; returns the K splits used.  ``schedule`` "stealing" draws the tiles from the
-    work-stealing queues (unsplit launches only)."""
+    work-stealing queues (unsplit launches only); ``b_stream`` 1 issues the LDS-DMA kernels' B copies
+    non-temporal."""
     if schedule == "streamk":
         tail = streamk_tail_for(workspace, cfg, dtype_code)
         if tail:
@@ -379,7 +383,7 @@ def _launch_grouped_fixed(workspace: GroupedWorkspace, cfg: KernelConfig, dtype_
                 workspace.a_ptrs.data_ptr(), workspace.b_ptrs.data_ptr(), workspace.c_ptrs.data_ptr(),
                 workspace.problem_count, m, n, k, dtype_code,
                 cfg.block_m, cfg.block_n, cfg.block_k, cfg.group_size_m, cfg.num_warps, cfg.num_stages, tail, grid,
-                1, scratch.data_ptr(), scratch.numel(), stream,
+                1, scratch.data_ptr(), scratch.numel(), b_stream, stream,
             )
             _native.check(status)
             return 1
@@ -398,7 +402,7 @@ def _launch_grouped_fixed(workspace: GroupedWorkspace, cfg: KernelConfig, dtype_
             workspace.problem_count, m, n, k, dtype_code,
             cfg.block_m, cfg.block_n, cfg.block_k, cfg.group_size_m, cfg.num_warps, cfg.num_stages, splits,
             max(1, min(tiles * splits, workspace.sm_count * cfg.cta_multiplier)), 1,
-            scratch.data_ptr(), scratch.numel(), stream,
+            scratch.data_ptr(), scratch.numel(), b_stream, stream,
         )
         _native.check(status)
         return splits
@@ -415,9 +419,9 @@ def _launch_grouped_fixed(workspace: GroupedWorkspace, cfg: KernelConfig, dtype_
     )
     if schedule == "stealing":
         queue = _native.tile_queue(workspace.a[0].device, stream)
-        status = lib.moegemm_grouped_gemm_stealing(*args, queue.data_ptr(), stream)
+        status = lib.moegemm_grouped_gemm_stealing(*args, queue.data_ptr(), b_stream, stream)
     elif schedule == "static":
-        status = lib.moegemm_grouped_gemm(*args, stream)
+        status = lib.moegemm_grouped_gemm(*args, b_stream, stream)
     else:
         raise ValueError(f"tile_schedule must be one of {_native.TILE_SCHEDULES}, got {schedule!r}")
     _native.check(status)
@@ -428,10 +432,10 @@ _GROUPED_AUTOTUNE_CACHE: dict[tuple, tuple] = {}
 
 
 def _grouped_tuning_key(workspace: GroupedWorkspace, scheduler: str, dtype_code: int, precision: int, split_k,
-                        tile_schedule) -> tuple:
+                        tile_schedule, b_stream=None) -> tuple:
     return (scheduler, workspace.problem_count, workspace.max_m, workspace.max_n, workspace.max_k,
             workspace.shape_signature, workspace.device_signature, workspace.sm_count, dtype_code, precision,
-            split_k, tile_schedule)
+            split_k, tile_schedule, b_stream)
 
 
 def launch_grouped(
@@ -442,6 +446,7 @@ def launch_grouped(
     autotune: bool = True,
     split_k: int | None = None,
     tile_schedule: str | None = None,
+    b_stream: int | None = None,
 ) -> None:
     """Launch the persistent grouped kernel (autotuned per workload key, or a fixed config).
 
@@ -453,8 +458,10 @@ def launch_grouped(
     with stealing) or "streamk" (whole tiles in exact rounds of one workgroup per CU, then the
     remaining tiles' K slices spread over every workgroup; homogeneous 16-bit groups whose tile
     count leaves a partial last round, static otherwise); None lets the tuner measure them
-    (static without autotuning).  ``workspace.tile_schedule`` records what ran.  G == 1 always
-    runs the single GEMM.
+    (static without autotuning).  ``workspace.tile_schedule`` records what ran.  ``b_stream``
+    (keyword-only, not in the reference's signature): 1 issues the LDS-DMA kernels' B copies
+    non-temporal, 0 as ordinary loads, None lets the tuner measure both on its finalists (0 without
+    autotuning); ``workspace.b_stream`` records what ran.  G == 1 always runs the single GEMM.
     """
     if split_k is not None and split_k < 1:
         raise ValueError("split_k must be None or a positive integer")
@@ -462,21 +469,24 @@ def launch_grouped(
         raise ValueError(f"tile_schedule must be None or one of {_native.GROUPED_SCHEDULES}, got {tile_schedule!r}")
     if tile_schedule in ("stealing", "streamk") and split_k is not None and split_k > 1:
         raise ValueError(f"the {tile_schedule} schedule runs unsplit launches only (split_k must be 1)")
+    if b_stream not in (None, 0, 1):
+        raise ValueError(f"b_stream must be None, 0 or 1, got {b_stream!r}")
     _require_runtime()
     cfg = config or workspace.config
     if workspace.problem_count == 1:
         launch_matmul(workspace.a[0], workspace.b[0], workspace.c[0], cfg, input_precision, autotune=autotune,
-                      split_k=split_k)
+                      split_k=split_k, b_stream=b_stream)
         workspace.config = last_matmul_config(cfg) if autotune else cfg
         workspace.scheduler = "single_problem_matmul"
         workspace.split_k = last_matmul_split()
         workspace.tile_schedule = last_matmul_schedule()
+        workspace.b_stream = last_matmul_b_stream()
         return
     dtype_code = _check_workspace(workspace)
     precision = _native.precision_code(input_precision, dtype_code)
     scheduler = "homogeneous_persistent" if workspace.homogeneous else "generic_persistent"
     if autotune:
-        key = _grouped_tuning_key(workspace, scheduler, dtype_code, precision, split_k, tile_schedule)
+        key = _grouped_tuning_key(workspace, scheduler, dtype_code, precision, split_k, tile_schedule, b_stream)
         tuned = _GROUPED_AUTOTUNE_CACHE.get(key)
         if tuned is None:
             candidates = grouped_candidate_configs(
@@ -490,16 +500,23 @@ def launch_grouped(
                 tile_schedule,
                 lambda cfg: streamk_tail_for(workspace, cfg, dtype_code) > 0,
             )
-            tuned = _tune(options, lambda o: _launch_grouped_fixed(workspace, o[0], dtype_code, precision, o[1], o[2]))
+            options = [(cfg, split, schedule, b_stream or 0) for cfg, split, schedule in options]
+            # The B copy policy is timed on the finalists where it is not pinned and the LDS-DMA kernels run.
+            twin = ((lambda o: (o[0], o[1], o[2], 1))
+                    if b_stream is None and _vector_layout(workspace, dtype_code) else None)
+            tuned = _tune(options, lambda o: _launch_grouped_fixed(workspace, o[0], dtype_code, precision, *o[1:]),
+                          twin=twin)
             _GROUPED_AUTOTUNE_CACHE[key] = tuned
-        cfg, split_k, schedule = tuned
+        cfg, split_k, schedule, stream_b = tuned
     else:
         schedule = tile_schedule or "static"
+        stream_b = b_stream or 0
         if schedule in ("stealing", "streamk") and split_k is None:
             split_k = 1
-    workspace.split_k = _launch_grouped_fixed(workspace, cfg, dtype_code, precision, split_k, schedule)
+    workspace.split_k = _launch_grouped_fixed(workspace, cfg, dtype_code, precision, split_k, schedule, stream_b)
     workspace.config = cfg
     workspace.scheduler = scheduler
+    workspace.b_stream = stream_b
     if schedule == "streamk" and not streamk_tail_for(workspace, cfg, dtype_code):
         schedule = "static"
     workspace.tile_schedule = schedule
@@ -537,7 +554,7 @@ def _swiglu_outputs(workspace: GroupedWorkspace):
     return workspace.h
 
 
-def _launch_swiglu_fixed(workspace: GroupedWorkspace, cfg: KernelConfig, dtype_code: int) -> None:
+def _launch_swiglu_fixed(workspace: GroupedWorkspace, cfg: KernelConfig, dtype_code: int, b_stream: int = 0) -> None:
     m, k, n = workspace.shapes[0]
     status = _native.library().moegemm_grouped_gemm_swiglu(
         workspace.a_ptrs.data_ptr(), workspace.b_ptrs.data_ptr(), workspace.h_ptrs.data_ptr(),
@@ -545,12 +562,12 @@ def _launch_swiglu_fixed(workspace: GroupedWorkspace, cfg: KernelConfig, dtype_c
         workspace.problem_count, m, n, k, 1 if workspace.homogeneous else 0,
         workspace.tile_count_for(cfg), dtype_code,
         cfg.block_m, cfg.block_n, cfg.block_k, cfg.group_size_m, cfg.num_warps, cfg.num_stages,
-        _grid_size(workspace, cfg), 1, _native.current_stream_handle(workspace.a[0].device),
+        _grid_size(workspace, cfg), 1, b_stream, _native.current_stream_handle(workspace.a[0].device),
     )
     _native.check(status)
 
 
-_SWIGLU_AUTOTUNE_CACHE: dict[tuple, KernelConfig] = {}
+_SWIGLU_AUTOTUNE_CACHE: dict[tuple, tuple[KernelConfig, int]] = {}
 
 
 def swiglu_candidate_configs(workspace: GroupedWorkspace) -> tuple[KernelConfig, ...]:
@@ -594,22 +611,27 @@ def launch_gate_up_swiglu(
     if autotune:
         key = ("swiglu", workspace.problem_count, workspace.max_m, workspace.max_n, workspace.max_k,
                workspace.shape_signature, workspace.device_signature, workspace.sm_count, dtype_code)
-        cfg = _SWIGLU_AUTOTUNE_CACHE.get(key)
-        if cfg is None:
-            # The plain W13 GEMM of the same workload, if already tuned, is the preferred tile: the
-            # activation changes only the epilogue, so a different pick would be timing noise.
+        tuned = _SWIGLU_AUTOTUNE_CACHE.get(key)
+        if tuned is None:
+            # The plain W13 GEMM of the same workload, if already tuned, gives the preferred tile and
+            # B copy policy: the activation changes only the epilogue, so a different pick would be
+            # timing noise.
             scheduler = "homogeneous_persistent" if workspace.homogeneous else "generic_persistent"
             plain = _GROUPED_AUTOTUNE_CACHE.get(_grouped_tuning_key(
                 workspace, scheduler, dtype_code, _native.PRECISION_IEEE, None, None))
-            candidates = list(swiglu_candidate_configs(workspace))
-            prefer = plain[0] if plain is not None and plain[0].tile_key in _native.swiglu_tiles(dtype_code) else None
+            allowed = _native.swiglu_tiles(dtype_code)
+            prefer = (plain[0], plain[3]) if plain is not None and plain[0].tile_key in allowed else None
+            candidates = [(c, 0) for c in swiglu_candidate_configs(workspace)]
             if prefer is not None and prefer not in candidates:
                 candidates.append(prefer)
-            cfg = _tune(candidates, lambda c: _launch_swiglu_fixed(workspace, c, dtype_code), prefer=prefer)
-            _SWIGLU_AUTOTUNE_CACHE[key] = cfg
-    elif cfg is None:
-        cfg = swiglu_candidate_configs(workspace)[0]
-    _launch_swiglu_fixed(workspace, cfg, dtype_code)
+            tuned = _tune(candidates, lambda o: _launch_swiglu_fixed(workspace, o[0], dtype_code, o[1]),
+                          prefer=prefer, twin=lambda o: (o[0], 1))
+            _SWIGLU_AUTOTUNE_CACHE[key] = tuned
+        cfg, stream_b = tuned
+    else:
+        cfg, stream_b = cfg or swiglu_candidate_configs(workspace)[0], 0
+    _launch_swiglu_fixed(workspace, cfg, dtype_code, stream_b)
     workspace.swiglu_config = cfg
+    workspace.swiglu_b_stream = stream_b
     workspace.scheduler = "homogeneous_persistent" if workspace.homogeneous else "generic_persistent"
     return outputs

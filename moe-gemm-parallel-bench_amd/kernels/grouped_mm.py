@@ -77,7 +77,7 @@ def _validate(mat_a, mat_b, offs, out):
 
 
 def _launch_fixed(mat_a, mat_b, offs, out, rows, k, n, groups, cfg: KernelConfig, dtype_code: int,
-                  precision: int, sm_count: int, schedule: str = "static") -> None:
+                  precision: int, sm_count: int, schedule: str = "static", b_stream: int = 0) -> None:
     grid = max(1, min(offsets_tile_bound(rows, groups, n, cfg.block_m, cfg.block_n), sm_count * cfg.cta_multiplier))
     stream = _native.current_stream_handle(mat_a.device)
     args = (
@@ -87,15 +87,16 @@ def _launch_fixed(mat_a, mat_b, offs, out, rows, k, n, groups, cfg: KernelConfig
     )
     if schedule == "stealing":
         queue = _native.tile_queue(mat_a.device, stream)
-        status = _native.library().moegemm_grouped_mm_offs_stealing(*args, queue.data_ptr(), stream)
+        status = _native.library().moegemm_grouped_mm_offs_stealing(*args, queue.data_ptr(), b_stream, stream)
     else:
-        status = _native.library().moegemm_grouped_mm_offs(*args, stream)
+        status = _native.library().moegemm_grouped_mm_offs(*args, b_stream, stream)
     _native.check(status)
 
 
-_OFFSETS_AUTOTUNE_CACHE: dict[tuple, tuple[KernelConfig, str]] = {}
+_OFFSETS_AUTOTUNE_CACHE: dict[tuple, tuple[KernelConfig, str, int]] = {}
 _LAST_CONFIG: list[KernelConfig | None] = [None]
 _LAST_SCHEDULE: list[str] = ["static"]
+_LAST_B_STREAM: list[int] = [0]
 
 
 def last_grouped_mm_config() -> KernelConfig | None:
@@ -108,8 +109,14 @@ def last_grouped_mm_schedule() -> str:
     return _LAST_SCHEDULE[0]
 
 
+def last_grouped_mm_b_stream() -> int:
+    """B copy policy of the most recent ``grouped_mm`` call: 1 = non-temporal B copies."""
+    return _LAST_B_STREAM[0]
+
+
 def grouped_mm(mat_a, mat_b, offs, *, out=None, config: KernelConfig | None = None,
-               input_precision: str = "ieee", autotune: bool = True, tile_schedule: str | None = None):
+               input_precision: str = "ieee", autotune: bool = True, tile_schedule: str | None = None,
+               b_stream: int | None = None):
     """C = per-group A @ B[e] over the expert-sorted layout; returns ``out`` (allocated if None).
 
     With ``autotune=True`` and no ``config``, the first call per (rows, K, N, G, strides, dtype)
@@ -117,11 +124,15 @@ def grouped_mm(mat_a, mat_b, offs, *, out=None, config: KernelConfig | None = No
     kernel launch.  The tuning key does not include ``offs``: the candidates are ranked for an
     even split of ``rows`` over the groups.  ``tile_schedule``: "static", "stealing" (per-XCD
     work-stealing tile queues), or None to let the tuner measure both (static otherwise).
+    ``b_stream``: 1 issues the LDS-DMA kernels' B copies non-temporal, 0 as ordinary loads, None lets
+    the tuner measure both on its finalists (0 without autotuning).
     """
     import torch
 
     if tile_schedule is not None and tile_schedule not in _native.TILE_SCHEDULES:
         raise ValueError(f"tile_schedule must be None or one of {_native.TILE_SCHEDULES}, got {tile_schedule!r}")
+    if b_stream not in (None, 0, 1):
+        raise ValueError(f"b_stream must be None, 0 or 1, got {b_stream!r}")
     rows, k, n, groups = _validate(mat_a, mat_b, offs, out)
     _require_runtime()
     if out is None:
@@ -135,22 +146,27 @@ def grouped_mm(mat_a, mat_b, offs, *, out=None, config: KernelConfig | None = No
 
     def launch(option):
         _launch_fixed(mat_a, mat_b, offs, out, rows, k, n, groups, option[0], dtype_code, precision, sm_count,
-                      option[1])
+                      option[1], option[2])
 
     if config is not None or not autotune:
-        option = (config or select_config(mean_m, n, k, mat_a.dtype), tile_schedule or "static")
+        option = (config or select_config(mean_m, n, k, mat_a.dtype), tile_schedule or "static", b_stream or 0)
     else:
         key = (rows, k, n, groups, tuple(mat_a.stride()), tuple(mat_b.stride()), tuple(out.stride()),
-               dtype_code, precision, _device_signature(mat_a.device), tile_schedule)
+               dtype_code, precision, _device_signature(mat_a.device), tile_schedule, b_stream)
         option = _OFFSETS_AUTOTUNE_CACHE.get(key)
         if option is None:
             candidates = grouped_candidate_configs(mean_m, n, k, problem_count=max(groups, 2), sm_count=sm_count,
                                                    dtype=mat_a.dtype)
             schedules = _native.TILE_SCHEDULES if tile_schedule is None else (tile_schedule,)
-            option = _tune([(cfg, schedule) for cfg in candidates for schedule in schedules], launch)
+            options = [(cfg, schedule, b_stream or 0) for cfg in candidates for schedule in schedules]
+            # The B copy policy is timed on the finalists where it is not pinned (16-bit operands; the
+            # general kernel ignores it).
+            sixteen = mat_a.dtype in (torch.float16, torch.bfloat16)
+            twin = (lambda o: (o[0], o[1], 1)) if b_stream is None and sixteen else None
+            option = _tune(options, launch, twin=twin)
             _OFFSETS_AUTOTUNE_CACHE[key] = option
     launch(option)
-    _LAST_CONFIG[0], _LAST_SCHEDULE[0] = option
+    _LAST_CONFIG[0], _LAST_SCHEDULE[0], _LAST_B_STREAM[0] = option
     return out
 
 
@@ -207,7 +223,7 @@ def grouped_mm_swiglu(mat_a, mat_b, offs, *, out=None, config: KernelConfig | No
             mat_a.data_ptr(), mat_b.data_ptr(), out.data_ptr(), offs.data_ptr(), groups, rows, n, k,
             mat_a.stride(0), mat_b.stride(0), mat_b.stride(1), out.stride(0), dtype_code,
             cfg.block_m, cfg.block_n, cfg.block_k, cfg.group_size_m, cfg.num_warps, cfg.num_stages, grid,
-            _native.current_stream_handle(mat_a.device),
+            0, _native.current_stream_handle(mat_a.device),
         )
         _native.check(status)
 

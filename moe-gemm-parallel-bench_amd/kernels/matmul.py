@@ -316,6 +316,7 @@ def with_split_options(configs, tiles_of, k: int, sm_count: int, split_k, splitt
 
 _LAST_SPLIT: list[int] = [1]
 _LAST_SCHEDULE: list[str] = ["static"]
+_LAST_B_STREAM: list[int] = [0]
 STREAMK = "streamk"  # split option of a tuning candidate: whole tiles in exact rounds, then a stream-K tail
 
 
@@ -329,6 +330,11 @@ def last_matmul_schedule() -> str:
     return _LAST_SCHEDULE[0]
 
 
+def last_matmul_b_stream() -> int:
+    """B copy policy of the most recent ``launch_matmul`` call: 1 = non-temporal B copies."""
+    return _LAST_B_STREAM[0]
+
+
 def _streamk_tail(a, b, c, m, n, k, cfg: KernelConfig) -> int:
     """Tail tiles of a stream-K launch of this GEMM on one workgroup per CU (0: not applicable)."""
     if not _vector_ok(a, b, c):
@@ -337,7 +343,7 @@ def _streamk_tail(a, b, c, m, n, k, cfg: KernelConfig) -> int:
     return _native.streamk_tail(tiles, _device_signature(a.device) % 1000, k, cfg.block_k)
 
 
-def _launch_fixed_streamk(a, b, c, m, n, k, cfg: KernelConfig, dtype_code: int, tail: int) -> None:
+def _launch_fixed_streamk(a, b, c, m, n, k, cfg: KernelConfig, dtype_code: int, tail: int, b_stream: int = 0) -> None:
     grid = _device_signature(a.device) % 1000
     stream = _native.current_stream_handle(a.device)
     workspace = _native.splitk_workspace(a.device, stream,
@@ -346,12 +352,12 @@ def _launch_fixed_streamk(a, b, c, m, n, k, cfg: KernelConfig, dtype_code: int, 
         a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k,
         a.stride(0), a.stride(1), b.stride(0), b.stride(1), c.stride(0), c.stride(1), dtype_code,
         cfg.block_m, cfg.block_n, cfg.block_k, cfg.group_size_m, cfg.num_warps, cfg.num_stages, tail, grid,
-        workspace.data_ptr(), workspace.numel(), stream,
+        workspace.data_ptr(), workspace.numel(), b_stream, stream,
     )
     _native.check(status)
 
 
-def _launch_fixed_splitk(a, b, c, m, n, k, cfg: KernelConfig, dtype_code: int, splits: int) -> None:
+def _launch_fixed_splitk(a, b, c, m, n, k, cfg: KernelConfig, dtype_code: int, splits: int, b_stream: int = 0) -> None:
     tiles = -(-m // cfg.block_m) * -(-n // cfg.block_n)
     nbytes = _native.splitk_workspace_bytes(tiles, splits, cfg.block_m, cfg.block_n)
     stream = _native.current_stream_handle(a.device)
@@ -360,19 +366,22 @@ def _launch_fixed_splitk(a, b, c, m, n, k, cfg: KernelConfig, dtype_code: int, s
         a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k,
         a.stride(0), a.stride(1), b.stride(0), b.stride(1), c.stride(0), c.stride(1), dtype_code,
         cfg.block_m, cfg.block_n, cfg.block_k, cfg.group_size_m, cfg.num_warps, cfg.num_stages, splits,
-        0, workspace.data_ptr(), workspace.numel(), stream,
+        0, workspace.data_ptr(), workspace.numel(), b_stream, stream,
     )
     _native.check(status)
 
 
-def _launch_fixed(a, b, c, m, n, k, cfg: KernelConfig, dtype_code: int, precision: int, split_k=None) -> int:
+def _launch_fixed(a, b, c, m, n, k, cfg: KernelConfig, dtype_code: int, precision: int, split_k=None,
+                  b_stream: int = 0) -> int:
     """One launch; returns the K splits used (``split_k`` None = ``splitk_count``'s choice,
-    ``STREAMK`` = a stream-K tail where one applies, else the unsplit launch)."""
+    ``STREAMK`` = a stream-K tail where one applies, else the unsplit launch).  ``b_stream`` 1 issues
+    the LDS-DMA kernels' B copies non-temporal."""
     _LAST_SCHEDULE[0] = "static"
+    _LAST_B_STREAM[0] = b_stream
     if split_k == STREAMK:
         tail = _streamk_tail(a, b, c, m, n, k, cfg) if precision == _native.PRECISION_IEEE else 0
         if tail:
-            _launch_fixed_streamk(a, b, c, m, n, k, cfg, dtype_code, tail)
+            _launch_fixed_streamk(a, b, c, m, n, k, cfg, dtype_code, tail, b_stream)
             _LAST_SCHEDULE[0] = STREAMK
             return 1
         split_k = 1
@@ -382,7 +391,7 @@ def _launch_fixed(a, b, c, m, n, k, cfg: KernelConfig, dtype_code: int, precisio
         splits = split_k if split_k is not None else splitk_count(tiles, k, cfg.block_k,
                                                                   _device_signature(a.device) % 1000)
     if splits > 1:
-        _launch_fixed_splitk(a, b, c, m, n, k, cfg, dtype_code, splits)
+        _launch_fixed_splitk(a, b, c, m, n, k, cfg, dtype_code, splits, b_stream)
         return splits
     lib = _native.library()
     status = lib.moegemm_matmul(
@@ -390,7 +399,7 @@ def _launch_fixed(a, b, c, m, n, k, cfg: KernelConfig, dtype_code: int, precisio
         a.stride(0), a.stride(1), b.stride(0), b.stride(1), c.stride(0), c.stride(1),
         dtype_code, precision,
         cfg.block_m, cfg.block_n, cfg.block_k, cfg.group_size_m, cfg.num_warps, cfg.num_stages,
-        0, _native.current_stream_handle(a.device),
+        0, b_stream, _native.current_stream_handle(a.device),
     )
     _native.check(status)
     return 1
@@ -405,12 +414,16 @@ def launch_matmul(
     *,
     autotune: bool = True,
     split_k: int | None = None,
+    b_stream: int | None = None,
 ) -> None:
     """Launch C = A @ B: autotuned per shape key, or with an explicit config when autotune is false.
 
     ``split_k`` (keyword-only, not in the reference's signature): None lets ``splitk_count`` split
     K when the output tiles leave most CUs idle (fp16/bf16 vector layouts, one launch with a
     deterministic in-kernel reduction); 1 disables it; n > 1 forces n splits.
+    ``b_stream`` (keyword-only, not in the reference's signature): 1 issues the LDS-DMA kernels' B
+    copies non-temporal, 0 as ordinary loads; None lets the tuner measure both (0 without
+    autotuning).  ``last_matmul_b_stream()`` reports what ran.
     """
     m, n, k = _validate_matrices(a, b, c)
     _require_runtime()
@@ -418,13 +431,15 @@ def launch_matmul(
     precision = _native.precision_code(input_precision, dtype_code)
     if split_k is not None and split_k < 1:
         raise ValueError("split_k must be None or a positive integer")
+    if b_stream not in (None, 0, 1):
+        raise ValueError(f"b_stream must be None, 0 or 1, got {b_stream!r}")
     if not autotune:
         cfg = config or select_config(m, n, k, a.dtype)
-        _LAST_SPLIT[0] = _launch_fixed(a, b, c, m, n, k, cfg, dtype_code, precision, split_k)
+        _LAST_SPLIT[0] = _launch_fixed(a, b, c, m, n, k, cfg, dtype_code, precision, split_k, b_stream or 0)
         return
     key = (
         m, n, k, tuple(a.stride()), tuple(b.stride()), tuple(c.stride()), dtype_code, precision,
-        _device_signature(a.device), split_k,
+        _device_signature(a.device), split_k, b_stream,
     )
     best = _AUTOTUNE_CACHE.get(key)
     if best is None:
@@ -434,10 +449,14 @@ def launch_matmul(
                                      sm_count, split_k, _vector_ok(a, b, c))
         if split_k is None:  # a stream-K tail where the tiles leave a partial last round
             options += [(cfg, STREAMK) for cfg in configs if _streamk_tail(a, b, c, m, n, k, cfg)]
-        best = _tune(options, lambda cand: _launch_fixed(a, b, c, m, n, k, cand[0], dtype_code, precision, cand[1]))
+        options = [(cfg, split, b_stream or 0) for cfg, split in options]
+        # The B copy policy is timed on the finalists where it is not pinned and the LDS-DMA kernels run.
+        twin = (lambda o: (o[0], o[1], 1)) if b_stream is None and _vector_ok(a, b, c) else None
+        best = _tune(options, lambda o: _launch_fixed(a, b, c, m, n, k, o[0], dtype_code, precision, o[1], o[2]),
+                     twin=twin)
         _AUTOTUNE_CACHE[key] = best
     _LAST_AUTOTUNED[0] = best[0]
-    _LAST_SPLIT[0] = _launch_fixed(a, b, c, m, n, k, best[0], dtype_code, precision, best[1])
+    _LAST_SPLIT[0] = _launch_fixed(a, b, c, m, n, k, best[0], dtype_code, precision, best[1], best[2])
 
 
 def _warm_clocks(launch, budget_ms: float = 100.0) -> None:
@@ -463,7 +482,7 @@ _FINALISTS = 5
 _FINAL_ROUNDS = 7
 
 
-def _tune(candidates, launch, prefer=None, prefer_margin: float = 0.03):
+def _tune(candidates, launch, prefer=None, prefer_margin: float = 0.03, twin=None):
     """Hot-time every candidate (graph replays, bounded) after a clock warm-up, twice (a forward and a
     reverse sweep), then re-time the best five interleaved (seven rounds of A, B, C, D, E) and keep
     the lowest median, so a clock drift during tuning shifts every finalist alike instead of
@@ -472,7 +491,9 @@ def _tune(candidates, launch, prefer=None, prefer_margin: float = 0.03):
 
     ``prefer`` (one of the candidates) always joins the finalists and is kept unless another
     finalist is faster by more than ``prefer_margin``: a choice already measured on the same
-    workload is not overturned by timing noise."""
+    workload is not overturned by timing noise.  ``twin(option)`` (or None) names a variant of a
+    finalist that only the interleaved rounds time, next to it: the non-temporal B copies, whose
+    effect depends on the workload but hardly on which of the leading tiles runs."""
     candidates = list(candidates)
     first: dict[int, float] = {}
     failed: set[int] = set()
@@ -502,6 +523,8 @@ def _tune(candidates, launch, prefer=None, prefer_margin: float = 0.03):
     finalists = [cfg for _, cfg in measured[:_FINALISTS]]
     if prefer is not None and prefer not in finalists and any(cfg == prefer for _, cfg in measured):
         finalists.append(prefer)
+    if twin is not None:
+        finalists += [t for t in dict.fromkeys(twin(cfg) for cfg in finalists) if t is not None and t not in finalists]
     rounds: list[list[float]] = [[] for _ in finalists]
     for _ in range(_FINAL_ROUNDS):
         for index, cfg in enumerate(finalists):

@@ -72,7 +72,7 @@ def _matmul(a, b, c, tile, grid):
     return lib.moegemm_matmul(
         a.data_ptr(), b.data_ptr(), c.data_ptr(), a.shape[0], b.shape[1], a.shape[1], a.stride(0), a.stride(1),
         b.stride(0), b.stride(1), c.stride(0), c.stride(1), native.DTYPE_BF16, 0, bm, bn, bk, 8, warps, stages,
-        grid, native.current_stream_handle(a.device))
+        grid, 0, native.current_stream_handle(a.device))
 
 
 def _offsets(a, b3, out, offs, tile, grid, queue=None):
@@ -83,8 +83,8 @@ def _offsets(a, b3, out, offs, tile, grid, queue=None):
             bm, bn, bk, 8, warps, stages, grid)
     stream = native.current_stream_handle(a.device)
     if queue is None:
-        return lib.moegemm_grouped_mm_offs(*args, stream)
-    return lib.moegemm_grouped_mm_offs_stealing(*args, queue.data_ptr(), stream)
+        return lib.moegemm_grouped_mm_offs(*args, 0, stream)
+    return lib.moegemm_grouped_mm_offs_stealing(*args, queue.data_ptr(), 0, stream)
 
 
 def test_single_gemm_with_a_over_4gib():
@@ -113,7 +113,7 @@ def test_single_gemm_with_a_over_4gib():
     native.check(lib.moegemm_matmul_streamk(
         a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, a.stride(0), 1, b.stride(0), 1, c.stride(0), 1,
         native.DTYPE_BF16, bm, bn, bk, 8, warps, stages, tail, grid, ws.data_ptr(), ws.numel(),
-        native.current_stream_handle(a.device)))
+        0, native.current_stream_handle(a.device)))
     torch.cuda.synchronize()
     _assert_product(c, a, b, "single stream-K")
     assert torch.isnan(guarded[m]).all()

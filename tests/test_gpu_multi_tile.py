@@ -67,7 +67,7 @@ def test_homogeneous_every_tile_small_grids_mixed_alignment(dtype):
             status = _native.library().moegemm_grouped_gemm(
                 ws.a_ptrs.data_ptr(), ws.b_ptrs.data_ptr(), ws.c_ptrs.data_ptr(), ws.dims.data_ptr(),
                 ws.strides.data_ptr(), groups, m, n, k, 1, tiles, code, 0, bm, bn, bk, 4, warps, stages, grid, 1,
-                _native.current_stream_handle(ws.a[0].device))
+                0, _native.current_stream_handle(ws.a[0].device))
             _native.check(status)
             torch.cuda.synchronize()
             for e, ((storage, lead), ref) in enumerate(zip(storages, expected)):
@@ -97,7 +97,7 @@ def test_single_every_tile_column_slice_small_grids(dtype, pitch_pad):
             status = _native.library().moegemm_matmul(
                 a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, a.stride(0), a.stride(1), b.stride(0),
                 b.stride(1), c.stride(0), c.stride(1), code, 0, bm, bn, bk, 4, warps, stages, grid,
-                _native.current_stream_handle(a.device))
+                0, _native.current_stream_handle(a.device))
             _native.check(status)
             torch.cuda.synchronize()
             label = f"tile {(bm, bn, bk, warps, stages)} grid {grid}"
@@ -144,9 +144,9 @@ def test_chained_two_stage_tiles_every_k_slice_count(k, schedule):
             stream = _native.current_stream_handle(ws.a[0].device)
             if schedule == "stealing":
                 queue = torch.zeros(_native.QUEUE_BYTES // 4, dtype=torch.int32, device="cuda")
-                status = _native.library().moegemm_grouped_gemm_stealing(*args, queue.data_ptr(), stream)
+                status = _native.library().moegemm_grouped_gemm_stealing(*args, queue.data_ptr(), 0, stream)
             else:
-                status = _native.library().moegemm_grouped_gemm(*args, stream)
+                status = _native.library().moegemm_grouped_gemm(*args, 0, stream)
             _native.check(status)
             torch.cuda.synchronize()
             if schedule == "stealing":
@@ -198,9 +198,9 @@ def test_chained_ping_pong_tiles_every_k_slice_count(k, schedule):
             stream = _native.current_stream_handle(ws.a[0].device)
             if schedule == "stealing":
                 queue = torch.zeros(_native.QUEUE_BYTES // 4, dtype=torch.int32, device="cuda")
-                status = _native.library().moegemm_grouped_gemm_stealing(*args, queue.data_ptr(), stream)
+                status = _native.library().moegemm_grouped_gemm_stealing(*args, queue.data_ptr(), 0, stream)
             else:
-                status = _native.library().moegemm_grouped_gemm(*args, stream)
+                status = _native.library().moegemm_grouped_gemm(*args, 0, stream)
             _native.check(status)
             torch.cuda.synchronize()
             if schedule == "stealing":
@@ -249,7 +249,7 @@ def test_ping_pong_swiglu_several_tiles_per_workgroup(k):
             status = _native.library().moegemm_grouped_gemm_swiglu(
                 ws.a_ptrs.data_ptr(), ws.b_ptrs.data_ptr(), h_ptrs.data_ptr(), ws.dims.data_ptr(),
                 ws.strides.data_ptr(), groups, m, n, k, 1, tiles, code, bm, bn, bk, 4, warps, stages, grid, 1,
-                _native.current_stream_handle(ws.a[0].device))
+                0, _native.current_stream_handle(ws.a[0].device))
             _native.check(status)
             torch.cuda.synchronize()
             results[grid] = [s[lead:lead + m * f].clone() for s, lead in storages]

@@ -284,9 +284,9 @@ def test_chained_tiles_on_ragged_offsets_small_grids(k, schedule):
             stream = _native.current_stream_handle(mat_a.device)
             if schedule == "stealing":
                 queue = torch.zeros(_native.QUEUE_BYTES // 4, dtype=torch.int32, device="cuda")
-                status = _native.library().moegemm_grouped_mm_offs_stealing(*args, queue.data_ptr(), stream)
+                status = _native.library().moegemm_grouped_mm_offs_stealing(*args, queue.data_ptr(), 0, stream)
             else:
-                status = _native.library().moegemm_grouped_mm_offs(*args, stream)
+                status = _native.library().moegemm_grouped_mm_offs(*args, 0, stream)
             _native.check(status)
             torch.cuda.synchronize()
             if schedule == "stealing":

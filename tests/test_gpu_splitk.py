@@ -217,7 +217,7 @@ def test_split_reduction_same_bits_whoever_reduces(tile, polls, monkeypatch):
             _native.check(lib.moegemm_matmul_splitk(
                 a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, a.stride(0), a.stride(1), b.stride(0),
                 b.stride(1), c.stride(0), c.stride(1), _native.DTYPE_BF16, bm, bn, bk, 8, warps, stages, splits,
-                grid, workspace.data_ptr(), workspace.numel(), stream))
+                grid, workspace.data_ptr(), workspace.numel(), 0, stream))
             torch.cuda.synchronize()
             assert not workspace[:256 * 1024].any(), f"counters not re-armed (grid {grid})"
             outputs.append(c)

@@ -50,7 +50,7 @@ def _launch_stealing(ws, cfg, grid, queue):
         ws.a_ptrs.data_ptr(), ws.b_ptrs.data_ptr(), ws.c_ptrs.data_ptr(), ws.dims.data_ptr(), ws.strides.data_ptr(),
         ws.problem_count, m, n, k, 1 if ws.homogeneous else 0, ws.tile_count_for(cfg), dtype_code, 0,
         cfg.block_m, cfg.block_n, cfg.block_k, cfg.group_size_m, cfg.num_warps, cfg.num_stages, grid,
-        1 if _vector_layout(ws, dtype_code) else 0, queue.data_ptr(), _native.current_stream_handle(ws.a[0].device))
+        1 if _vector_layout(ws, dtype_code) else 0, queue.data_ptr(), 0, _native.current_stream_handle(ws.a[0].device))
     _native.check(status)
 
 
@@ -116,7 +116,7 @@ def test_offsets_many_groups_steal_across_prefix_chunks_and_clamped_count():
                 mat_a.data_ptr(), mat_b.data_ptr(), out.data_ptr(), offs.data_ptr(), groups, rows, n, k,
                 mat_a.stride(0), mat_b.stride(0), mat_b.stride(1), out.stride(0), _native.DTYPE_BF16, 0,
                 cfg.block_m, cfg.block_n, cfg.block_k, cfg.group_size_m, cfg.num_warps, cfg.num_stages, grid,
-                queue.data_ptr(), _native.current_stream_handle(mat_a.device))
+                queue.data_ptr(), 0, _native.current_stream_handle(mat_a.device))
             _native.check(status)
             torch.cuda.synchronize()
             got = out.double().cpu()

@@ -53,7 +53,7 @@ def _matmul_streamk(a, b, c, tile, tail, grid, ws, group_m=8):
         a.data_ptr(), b.data_ptr(), c.data_ptr(), a.shape[0], b.shape[1], a.shape[1],
         a.stride(0), a.stride(1), b.stride(0), b.stride(1), c.stride(0), c.stride(1), native.dtype_code(a.dtype),
         bm, bn, bk, group_m, warps, stages, tail, grid, ws.data_ptr(), ws.numel(),
-        native.current_stream_handle(a.device))
+        0, native.current_stream_handle(a.device))
 
 
 def _grouped_streamk(a_list, b_list, c_list, tile, tail, grid, ws, group_m=8):
@@ -66,7 +66,7 @@ def _grouped_streamk(a_list, b_list, c_list, tile, tail, grid, ws, group_m=8):
     status = lib.moegemm_grouped_gemm_streamk(
         tables[0].data_ptr(), tables[1].data_ptr(), tables[2].data_ptr(), len(a_list), m, n, k,
         native.dtype_code(a_list[0].dtype), bm, bn, bk, group_m, warps, stages, tail, grid, 1,
-        ws.data_ptr(), ws.numel(), native.current_stream_handle(a_list[0].device))
+        ws.data_ptr(), ws.numel(), 0, native.current_stream_handle(a_list[0].device))
     return status, tables  # the tables must outlive the launch
 
 

@@ -65,13 +65,13 @@ def test_compiled_menus_match_python_candidate_pools():
 
 def _grouped(**overrides):
     args = dict(a=1, b=1, c=1, dims=1, strides=1, g=4, m=16, n=64, k=64, homog=1, tiles=4, dtype=1, prec=0,
-                bm=256, bn=256, bk=64, group=8, warps=8, stages=2, grid=4, vec=1, stream=None)
+                bm=256, bn=256, bk=64, group=8, warps=8, stages=2, grid=4, vec=1, b_stream=0, stream=None)
     args.update(overrides)
     lib = _native.library()
     return lib.moegemm_grouped_gemm(args["a"], args["b"], args["c"], args["dims"], args["strides"], args["g"],
                                     args["m"], args["n"], args["k"], args["homog"], args["tiles"], args["dtype"],
                                     args["prec"], args["bm"], args["bn"], args["bk"], args["group"], args["warps"],
-                                    args["stages"], args["grid"], args["vec"], args["stream"])
+                                    args["stages"], args["grid"], args["vec"], args["b_stream"], args["stream"])
 
 
 @pytest.mark.parametrize("override, code, needle", [
@@ -86,6 +86,8 @@ def _grouped(**overrides):
     ({"m": 0}, _native.ERR_INVALID, "shape"),
     ({"homog": 0, "dims": None}, _native.ERR_INVALID, "dims"),
     ({"homog": 0, "tiles": -1}, _native.ERR_INVALID, "total_tiles"),
+    ({"b_stream": 2}, _native.ERR_INVALID, "b_stream"),
+    ({"b_stream": -1}, _native.ERR_INVALID, "b_stream"),
 ])
 def test_grouped_entry_rejects_bad_arguments_without_launching(override, code, needle):
     assert _grouped(**override) == code
@@ -100,7 +102,7 @@ def test_matmul_entry_rejects_bad_arguments_without_launching():
     lib = _native.library()
     call = lambda **kw: lib.moegemm_matmul(
         kw.get("a", 1), 1, 1, kw.get("m", 4), 4, 4, 4, 1, 4, 1, 4, 1, kw.get("dtype", 1), 0,
-        kw.get("bm", 16), 64, 128, 1, 4, 4, 0, None)
+        kw.get("bm", 16), 64, 128, 1, 4, 4, 0, 0, None)
     assert call(m=0) == _native.ERR_INVALID and "shape" in _native.last_error()
     assert call(a=None) == _native.ERR_INVALID and "non-null" in _native.last_error()
     assert call(bm=24) == _native.ERR_NO_KERNEL
@@ -122,7 +124,7 @@ def test_fast_layout_byte_limits_match_the_python_mirror(m, sam, sbk, scm):
     k, n = 256, 64
     status = _native.library().moegemm_matmul_splitk(
         4096, 8192, 12288, m, n, k, sam, 1, sbk, 1, scm, 1, _native.DTYPE_BF16, 256, 256, 32, 8, 8, 4, 2, 0,
-        None, 0, None)
+        None, 0, 0, None)
     assert status == _native.ERR_INVALID
     accepted = "workspace" in _native.last_error()
     assert accepted != ("vector layout" in _native.last_error())
@@ -195,21 +197,21 @@ def test_splitk_entry_rejects_more_tiles_than_counters_without_launching():
     lib = _native.library()
     m, n, k = 4096, 16448, 1024  # 256 x 257 tiles of 16 x 64: one more column than the counters hold
     status = lib.moegemm_matmul_splitk(256, 256, 256, m, n, k, k, 1, n, 1, n, 1, _native.DTYPE_BF16,
-                                       16, 64, 128, 1, 4, 4, 2, 0, None, 0, None)
+                                       16, 64, 128, 1, 4, 4, 2, 0, None, 0, 0, None)
     assert status == _native.ERR_INVALID and "output tiles" in _native.last_error()
 
 
 def test_stealing_entries_reject_a_missing_or_misaligned_queue_without_launching():
     lib = _native.library()
     args = (1, 1, 1, 1, 1, 4, 16, 64, 64, 1, 4, _native.DTYPE_BF16, 0, 16, 64, 128, 1, 4, 4, 4, 1)
-    assert lib.moegemm_grouped_gemm_stealing(*args, None, None) == _native.ERR_INVALID
+    assert lib.moegemm_grouped_gemm_stealing(*args, None, 0, None) == _native.ERR_INVALID
     assert "tile queue" in _native.last_error()
-    assert lib.moegemm_grouped_gemm_stealing(*args, 4, None) == _native.ERR_INVALID
+    assert lib.moegemm_grouped_gemm_stealing(*args, 4, 0, None) == _native.ERR_INVALID
     assert "256-byte aligned" in _native.last_error()
     offs_args = (256, 256, 256, 256, 2, 16, 64, 64, 64, 64 * 64, 64, 64, _native.DTYPE_BF16, 0, 16, 64, 128, 1, 4, 4, 4)
-    assert lib.moegemm_grouped_mm_offs_stealing(*offs_args, None, None) == _native.ERR_INVALID
+    assert lib.moegemm_grouped_mm_offs_stealing(*offs_args, None, 0, None) == _native.ERR_INVALID
     assert "tile queue" in _native.last_error()
-    assert lib.moegemm_grouped_mm_offs_stealing(*offs_args, 260, None) == _native.ERR_INVALID
+    assert lib.moegemm_grouped_mm_offs_stealing(*offs_args, 260, 0, None) == _native.ERR_INVALID
     assert "256-byte aligned" in _native.last_error()
 
 

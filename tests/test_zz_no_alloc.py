@@ -54,8 +54,8 @@ def test_noalloc_splitk_matches_the_workspace_entry_point_twice():
         nbytes = _native.splitk_workspace_bytes(tiles, splits, tile[0], tile[1])
         workspace = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
         _native.check(lib.moegemm_matmul_splitk(*_args(a, b, expected, tile, splits), workspace.data_ptr(),
-                                                workspace.numel(), stream))
-        _native.check(lib.moegemm_matmul_splitk_noalloc(*_args(a, b, got, tile, splits), stream))
+                                                workspace.numel(), 0, stream))
+        _native.check(lib.moegemm_matmul_splitk_noalloc(*_args(a, b, got, tile, splits), 0, stream))
         torch.cuda.synchronize()
         assert torch.isfinite(got).all()
         assert torch.equal(got, expected)
@@ -70,7 +70,7 @@ def test_noalloc_splitk_rejects_partials_beyond_the_static_area():
     b = torch.zeros((4096, 4096), device="cuda", dtype=torch.bfloat16)
     c = torch.zeros((4096, 4096), device="cuda", dtype=torch.bfloat16)
     status = lib.moegemm_matmul_splitk_noalloc(*_args(a, b, c, (256, 256, 64, 8, 2), 4),
-                                               ctypes.c_void_p(_native.current_stream_handle(a.device)))
+                                               0, ctypes.c_void_p(_native.current_stream_handle(a.device)))
     assert status == _native.ERR_INVALID
     assert "static area" in _native.last_error()
     torch.cuda.synchronize()
