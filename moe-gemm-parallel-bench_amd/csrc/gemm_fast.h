@@ -227,7 +227,9 @@ struct FastTile {
   }
 
   // Copy K slice [k0, k0 + BK) into LDS stage `stage`.
-  // Slot j of a stage is written by wave j % NW; `wave` below is wave-uniform.
+  // Slot j of a stage is written by wave j % NW; `wave` below is wave-uniform.  NTB fixes B's copy
+  // policy at compile time (0 ordinary, 1 non-temporal); -1 reads d.b_stream at run time.
+  template <int NTB = -1>
   __device__ static __forceinline__ void issue_stage(const Dma& d, int stage, int k0) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t base = d.lds_wave + (uint32_t)(stage * STAGE_BYTES);
@@ -240,7 +242,9 @@ struct FastTile {
       }
     }
     const uint32_t kstep = (uint32_t)k0 * d.ldb_bytes;
-    if (d.b_stream)
+    if constexpr (NTB >= 0)
+      issue_b<NTB == 1>(d, base, kstep, wave);
+    else if (d.b_stream)
       issue_b<true>(d, base, kstep, wave);
     else
       issue_b<false>(d, base, kstep, wave);

@@ -55,14 +55,19 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
   template <int EPI, class Hook>
   __device__ static __forceinline__ void run_tile(const ProblemDesc& pd, int tm, int tn, char* smem, bool tf32,
                                                   Hook&& before_store) {
-    // Each group runs a copy of the schedule compiled for it (no group tests inside the K loop).
-    if (__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) >= NW / 2)
-      group_tile<EPI, true>(pd, tm, tn, smem, before_store);
-    else
-      group_tile<EPI, false>(pd, tm, tn, smem, before_store);
+    // Each group runs a copy of the schedule compiled for it and for the launch's B copy policy
+    // (no group or policy tests inside the K loop).
+    const bool second = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) >= NW / 2;
+    if (pd.b_stream) {
+      if (second) group_tile<EPI, true, 1>(pd, tm, tn, smem, before_store);
+      else group_tile<EPI, false, 1>(pd, tm, tn, smem, before_store);
+    } else {
+      if (second) group_tile<EPI, true, 0>(pd, tm, tn, smem, before_store);
+      else group_tile<EPI, false, 0>(pd, tm, tn, smem, before_store);
+    }
   }
 
-  template <int EPI, bool SECOND, class Hook>
+  template <int EPI, bool SECOND, int NTB, class Hook>
   __device__ static __forceinline__ void group_tile(const ProblemDesc& pd, int tm, int tn, char* smem,
                                                     Hook&& before_store) {
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -82,7 +87,7 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
 
     // Prologue: slices 0..S-1 in flight; slice 0 published by barrier 0.
 #pragma unroll
-    for (int s = 0; s < STAGES; ++s) Base::issue_stage(d, s, s * BK);
+    for (int s = 0; s < STAGES; ++s) Base::template issue_stage<NTB>(d, s, s * BK);
     wait_vmcnt<(STAGES - 1) * XMIN>();
     phase_barrier();
     if constexpr (second) phase_barrier();  // group 1 runs one barrier behind
@@ -92,7 +97,7 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
     for (int kt = 0; kt < kt_count; ++kt) {
       // Memory phase.
       const char* cur = smem + (kt % STAGES) * STAGE_BYTES;
-      if (kt >= 1) Base::issue_stage(d, (kt - 1) % STAGES, (kt - 1 + STAGES) * BK);
+      if (kt >= 1) Base::template issue_stage<NTB>(d, (kt - 1) % STAGES, (kt - 1 + STAGES) * BK);
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk)
         Base::load_frags(af[kk], bf[kk], cur, cur + A_BYTES, kk, wave_m, wave_n, pd.swiglu != 0);
@@ -155,12 +160,18 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
     static_assert(CHAIN_OK, "the chained epilogue stages C in one stage's slots");
     // Each group runs a copy of the tile's schedule compiled for it, so the group tests of the K
     // steps (which wait comes where, the extra barriers) cost no branches.
-    if (__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) >= NW / 2)
-      return chained_group<true>(pd, tm, tn, smem, ch, sched, next, ntm, ntn);
-    return chained_group<false>(pd, tm, tn, smem, ch, sched, next, ntm, ntn);
+    // The B copy policy is uniform over a launch, so the next tile's prefetched slices take this
+    // tile's.
+    const bool second = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) >= NW / 2;
+    if (pd.b_stream) {
+      if (second) return chained_group<true, 1>(pd, tm, tn, smem, ch, sched, next, ntm, ntn);
+      return chained_group<false, 1>(pd, tm, tn, smem, ch, sched, next, ntm, ntn);
+    }
+    if (second) return chained_group<true, 0>(pd, tm, tn, smem, ch, sched, next, ntm, ntn);
+    return chained_group<false, 0>(pd, tm, tn, smem, ch, sched, next, ntm, ntn);
   }
 
-  template <bool SECOND, class Sched>
+  template <bool SECOND, int NTB, class Sched>
   __device__ static __forceinline__ bool chained_group(const ProblemDesc& pd, int tm, int tn, char* smem, Chain& ch,
                                                        Sched& sched, ProblemDesc& next, int& ntm, int& ntn) {
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -193,7 +204,7 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
       sched.started();
       sched.before_barrier();
 #pragma unroll
-      for (int s = 0; s < STAGES; ++s) Base::issue_stage(d, s, s * BK);
+      for (int s = 0; s < STAGES; ++s) Base::template issue_stage<NTB>(d, s, s * BK);
       wait_vmcnt<(STAGES - 1) * XMIN>();
     }
     phase_barrier();
@@ -215,14 +226,14 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
       const char* cur = smem + ((kt + rot) & (STAGES - 1)) * STAGE_BYTES;
       const int buf = (kt - 1 + rot) & (STAGES - 1), s = kt - 1 + STAGES;
       if constexpr (ISSUE == 1) {
-        Base::issue_stage(d, buf, s * BK);
+        Base::template issue_stage<NTB>(d, buf, s * BK);
       } else if constexpr (ISSUE == 2) {
         if (chain && s >= kt_count) {
           Dma dn;  // the next tile's copy state, recomputed for each of its first slices
           Base::setup_dma(dn, next, ntm * BM, ntn * BN, smem);
-          Base::issue_stage(dn, buf, (s - kt_count) * BK);
+          Base::template issue_stage<NTB>(dn, buf, (s - kt_count) * BK);
         } else {
-          Base::issue_stage(d, buf, s * BK);
+          Base::template issue_stage<NTB>(d, buf, s * BK);
         }
       }
 #pragma unroll
@@ -262,7 +273,7 @@ struct PingPongTile : FastTile<E, 256, 256, BK_, 2, 4, STAGES_> {
       {
         Dma dn;
         Base::setup_dma(dn, next, ntm * BM, ntn * BN, smem);
-        Base::issue_stage(dn, last, (STAGES - 1) * BK);
+        Base::template issue_stage<NTB>(dn, last, (STAGES - 1) * BK);
       }
       if constexpr (!second) phase_barrier();
       ch.rot = (kt_count + rot) & (STAGES - 1);

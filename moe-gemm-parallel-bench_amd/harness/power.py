@@ -120,6 +120,9 @@ def main(argv=None) -> int:
     parser.add_argument("--sample-every", type=float, default=0.2)
     parser.add_argument("--workloads", default="grouped,single,hipblaslt")
     parser.add_argument("--kernel-config", default=None, metavar="BM,BN,BK,WARPS,STAGES,GROUP_M,MULT")
+    parser.add_argument("--b-stream", type=int, choices=(0, 1), default=None,
+                        help="B copy policy of this project's launches (1 = non-temporal B copies); "
+                             "default: the tuner's choice, or 0 with --kernel-config")
     args = parser.parse_args(argv)
     workloads = [w for w in args.workloads.split(",") if w]
     unknown = sorted(set(workloads) - set(WORKLOADS))
@@ -139,17 +142,18 @@ def main(argv=None) -> int:
         dws = build_grouped_workspace([DECODE_SHAPE] * EXPERTS, dtype, seed=1234)
         flops_of["decode"] = 2 * EXPERTS * DECODE_SHAPE[0] * DECODE_SHAPE[1] * DECODE_SHAPE[2]
         if pinned is None:
-            launch_grouped(dws)
-            steps["decode"] = lambda: launch_grouped(dws)
+            launch_grouped(dws, b_stream=args.b_stream)
+            steps["decode"] = lambda: launch_grouped(dws, b_stream=args.b_stream)
         else:
-            steps["decode"] = lambda: launch_grouped(dws, config=pinned, autotune=False)
+            steps["decode"] = lambda: launch_grouped(dws, config=pinned, autotune=False, b_stream=args.b_stream)
     if "grouped" in workloads:
         ws = build_grouped_workspace([GROUPED_SHAPE] * EXPERTS, dtype, seed=1234)
         if pinned is None:
-            launch_grouped(ws)  # autotune once, outside the measurement
-            steps["grouped"] = lambda: launch_grouped(ws)
+            launch_grouped(ws, b_stream=args.b_stream)  # autotune once, outside the measurement
+            steps["grouped"] = lambda: launch_grouped(ws, b_stream=args.b_stream)
+            print(f"grouped: autotuned {ws.config}, schedule {ws.tile_schedule}, b_stream {ws.b_stream}", flush=True)
         else:
-            steps["grouped"] = lambda: launch_grouped(ws, config=pinned, autotune=False)
+            steps["grouped"] = lambda: launch_grouped(ws, config=pinned, autotune=False, b_stream=args.b_stream)
     if "hipblaslt_batched" in workloads:
         gen = torch.Generator(device="cuda").manual_seed(1234)
         gm, gk, gn = GROUPED_SHAPE
@@ -164,10 +168,11 @@ def main(argv=None) -> int:
         c = torch.empty(m, n, device="cuda", dtype=dtype)
         if "single" in workloads:
             if pinned is None:
-                launch_matmul(a, b, c)
-                steps["single"] = lambda: launch_matmul(a, b, c)
+                launch_matmul(a, b, c, b_stream=args.b_stream)
+                steps["single"] = lambda: launch_matmul(a, b, c, b_stream=args.b_stream)
             else:
-                steps["single"] = lambda: launch_matmul(a, b, c, config=pinned, autotune=False)
+                steps["single"] = lambda: launch_matmul(a, b, c, config=pinned, autotune=False,
+                                                        b_stream=args.b_stream)
         if "hipblaslt" in workloads:
             steps["hipblaslt"] = lambda: torch.mm(a, b, out=c)
 
