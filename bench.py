@@ -129,23 +129,26 @@ def _timed(step, steps: int, warmup: int, settle_s: float = 0.0) -> tuple[float,
 
 
 def _case(projection: str, parallel_type: str, m: int, steps: int, warmup: int, seed: int = 1234,
-          pinned=None, model: str = "dsv3", settle_s: float = 0.0) -> dict:
-    """Time one case of a BASELINE.json model (DSV3 by default); ``pinned`` (a KernelConfig) skips autotuning."""
+          pinned=None, model: str = "dsv3", settle_s: float = 0.0, b_stream=None) -> dict:
+    """Time one case of a BASELINE.json model (DSV3 by default); ``pinned`` (a KernelConfig) skips autotuning.
+
+    ``b_stream`` pins the B copy policy (None: the tuner times both; with ``pinned``, 0)."""
     import torch
 
     from kernels.grouped_gemm import launch_grouped
     from utils.metrics import gemm_bytes, gemm_flops
 
     workspace = _workspace(projection, parallel_type, m, seed, model)
-    launch_grouped(workspace, config=pinned, autotune=pinned is None)  # autotune (untimed) on a cache miss
-    for c in workspace.c:
-        c.fill_(float("nan"))
-    launch_grouped(workspace, config=pinned, autotune=pinned is None)
-    torch.cuda.synchronize()
-    error = _check_sample(workspace)
 
     def step():
-        launch_grouped(workspace, config=pinned, autotune=pinned is None)
+        launch_grouped(workspace, config=pinned, autotune=pinned is None, b_stream=b_stream)
+
+    step()  # autotune (untimed) on a cache miss
+    for c in workspace.c:
+        c.fill_(float("nan"))
+    step()
+    torch.cuda.synchronize()
+    error = _check_sample(workspace)
 
     cold_ms, _ = _timed(step, steps, warmup)  # straight after the idle check, no settle period
     ms, wall_ms = _timed(step, steps, warmup, settle_s)
@@ -306,12 +309,17 @@ def _mfma_busy_from_profiles(case: str):
             "source": f"profiles/{path.name}"}
 
 
-def _traffic_from_profiles(case: str):
-    """HBM bytes per launch recorded by a committed rocprofv3 counter summary, if any."""
+def _traffic_from_profiles(case: str, b_stream: int = 0):
+    """HBM bytes per launch recorded by a committed rocprofv3 counter summary, if any.
+
+    A summary may give one figure per B copy policy (``traffic_bytes_per_launch_b_stream_1: ...``);
+    the plain ``traffic_bytes_per_launch: ...`` line serves a policy without one."""
     path = REPO / "profiles" / f"{case}_hbm_traffic.md"
     if not path.exists():
         return None
-    match = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", path.read_text())
+    text = path.read_text()
+    match = (re.search(rf"traffic_bytes_per_launch_b_stream_{b_stream}:\s*([0-9.eE+]+)", text)
+             or re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", text))
     return float(match.group(1)) if match else None
 
 
@@ -439,6 +447,9 @@ def main(argv=None) -> int:
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--kernel-config", metavar="BM,BN,BK,WARPS,STAGES,GROUP_M,MULT", default=None,
                         help="pin the headline kernel config instead of autotuning (counter passes)")
+    parser.add_argument("--b-stream", type=int, choices=(0, 1), default=None,
+                        help="pin the headline's B copy policy (1 non-temporal); with --kernel-config the "
+                             "default is 0, else the tuner times both")
     parser.add_argument("--case", metavar="PROJ,PAR,M", default=None,
                         help="only time one case (e.g. W1,EP,8) of --model, print its row and exit (profiling); "
                              "--kernel-config pins its kernel")
@@ -476,10 +487,11 @@ def main(argv=None) -> int:
         if projection not in ("W1", "W2") or parallel_type not in ("EP", "TP"):
             raise SystemExit("--case takes PROJ,PAR,M with PROJ in W1/W2 and PAR in EP/TP")
         row = _case(projection, parallel_type, int(m), args.steps, args.warmup, pinned=pinned, model=args.model,
-                    settle_s=args.settle_seconds)
+                    settle_s=args.settle_seconds, b_stream=args.b_stream)
         print(json.dumps(row))
         return 0 if row["correct"] else 1
-    headline = _case("W1", "EP", 512, args.steps, args.warmup, pinned=pinned, settle_s=args.settle_seconds)
+    headline = _case("W1", "EP", 512, args.steps, args.warmup, pinned=pinned, settle_s=args.settle_seconds,
+                     b_stream=args.b_stream)
     _progress(headline)
     case_settle = args.settle_seconds / 2
     cases = []
@@ -492,7 +504,7 @@ def main(argv=None) -> int:
         cases.append(_progress(_swiglu_case(512, max(5, args.steps // 2), 2, settle_s=case_settle)))
         for mean_rows in (512, 64):
             cases.append(_progress(_ragged_case(max(5, args.steps // 2), 2, settle_s=case_settle, mean_rows=mean_rows)))
-    traffic = _traffic_from_profiles(headline["case"])
+    traffic = _traffic_from_profiles(headline["case"], headline["b_stream"])
     tp = next((c for c in cases if c["case"] == "dsv3_w1_tp_me512"), None)
     by_case = {c["case"]: c for c in cases + [headline]}
     # TP TFLOP/s over EP TFLOP/s at equal per-rank FLOPs (the reference's EP/TP comparison).

@@ -269,3 +269,22 @@ def test_power_harness_parses_amd_smi_and_kernel_config():
     assert (cfg.block_m, cfg.block_n, cfg.block_k, cfg.num_warps, cfg.num_stages, cfg.group_size_m,
             cfg.cta_multiplier) == (256, 256, 32, 8, 4, 8, 1)
     assert parse_kernel_config(None) is None
+
+
+def test_bench_reads_the_traffic_figure_of_the_policy_that_ran():
+    """bench.py's roofline.traffic comes from the committed counter summary of the headline, which
+    gives one figure per B copy policy; a policy without its own line takes the plain one."""
+    import importlib.util
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    spec = importlib.util.spec_from_file_location("bench_under_test", root / "bench.py")
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    case = "dsv3_w1_ep_me512"
+    ordinary, streamed = bench._traffic_from_profiles(case, 0), bench._traffic_from_profiles(case, 1)
+    algorithmic = 2 * 32 * (512 * 7168 + 7168 * 4096 + 512 * 4096)
+    assert ordinary is not None and streamed is not None and ordinary != streamed
+    for measured in (ordinary, streamed):
+        assert abs(measured / algorithmic - 1) < 0.01
+    assert bench._traffic_from_profiles("no_such_case", 1) is None
