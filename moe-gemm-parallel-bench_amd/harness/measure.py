@@ -149,14 +149,15 @@ def _measure_layout(case, members, settings, env) -> list[dict]:
                   f"{row['skip_reason'] or row['error']}", flush=True)
         elif row.get("block_m"):
             # What ran, for the log (the CSV keeps the reference's columns): the tile config, and the
-            # tile schedule and K splits the last launch of the HIP workspace recorded.
+            # tile schedule, K splits and B copy policy the last launch of the HIP workspace recorded.
             schedule = getattr(ring[0], "tile_schedule", None)
             splits = getattr(ring[0], "split_k", None)
+            streamed = getattr(ring[0], "b_stream", 0)
             print(f"  {provider.name}/{row['mode']}: {row['block_m']}x{row['block_n']}x{row['block_k']} "
                   f"{row['num_warps']} waves {row['num_stages']} stages GROUP_M {row['group_size_m']} "
                   f"x{row['cta_multiplier']}" + (f" {schedule}" if schedule else "")
                   + (f" split {splits}" if splits and splits > 1 else "")
-                  + f": {row['latency_ms'] * 1e3:.1f} us", flush=True)
+                  + (" nt-B" if streamed else "") + f": {row['latency_ms'] * 1e3:.1f} us", flush=True)
     del ring
     torch.cuda.empty_cache()
     return rows
