@@ -82,20 +82,38 @@ class GroupedWorkspace:
     def problem_count(self) -> int:
         return len(self.a)
 
+    def _shape_stats(self) -> tuple:
+        """(shapes, (max M, max N, max K), tile counts by (BM, BN)), kept while ``shapes`` is the same
+        tuple object: every launch reads them, and over hundreds of problems recomputing them costs
+        as much host time as a decode-sized kernel runs."""
+        cached = self.__dict__.get("_shape_stats_cache")
+        if cached is None or cached[0] is not self.shapes:
+            shapes = self.shapes
+            maxima = (max(m for m, _, _ in shapes), max(n for _, _, n in shapes), max(k for _, k, _ in shapes))
+            cached = (shapes, maxima, {})
+            self.__dict__["_shape_stats_cache"] = cached
+        return cached
+
     @property
     def max_m(self) -> int:
-        return max(m for m, _, _ in self.shapes)
+        return self._shape_stats()[1][0]
 
     @property
     def max_n(self) -> int:
-        return max(n for _, _, n in self.shapes)
+        return self._shape_stats()[1][1]
 
     @property
     def max_k(self) -> int:
-        return max(k for _, k, _ in self.shapes)
+        return self._shape_stats()[1][2]
 
     def tile_count_for(self, config: KernelConfig) -> int:
-        return sum(math.ceil(m / config.block_m) * math.ceil(n / config.block_n) for m, _, n in self.shapes)
+        shapes, _, counts = self._shape_stats()
+        key = (config.block_m, config.block_n)
+        count = counts.get(key)
+        if count is None:
+            count = counts[key] = sum(math.ceil(m / config.block_m) * math.ceil(n / config.block_n)
+                                      for m, _, n in shapes)
+        return count
 
     @property
     def tile_count(self) -> int:
@@ -331,8 +349,10 @@ def _check_workspace(workspace: GroupedWorkspace) -> int:
     return _native.dtype_code(a0.dtype)
 
 
-def _grouped_splits(workspace: GroupedWorkspace, cfg: KernelConfig, dtype_code: int, split_k) -> int:
-    if not workspace.homogeneous or not _vector_layout(workspace, dtype_code):
+def _grouped_splits(workspace: GroupedWorkspace, cfg: KernelConfig, dtype_code: int, split_k, vector=None) -> int:
+    if vector is None:
+        vector = _vector_layout(workspace, dtype_code)
+    if not workspace.homogeneous or not vector:
         return 1
     if split_k is not None:
         return split_k
@@ -388,7 +408,8 @@ def _launch_grouped_fixed(workspace: GroupedWorkspace, cfg: KernelConfig, dtype_
             _native.check(status)
             return 1
         schedule = "static"  # no partial last round: the static launch is the same work
-    splits = _grouped_splits(workspace, cfg, dtype_code, split_k)
+    vector = _vector_layout(workspace, dtype_code)
+    splits = _grouped_splits(workspace, cfg, dtype_code, split_k, vector)
     if schedule == "stealing" and splits > 1:
         raise ValueError("the work-stealing schedule runs unsplit launches only (split_k must be 1)")
     if splits > 1:
@@ -415,7 +436,7 @@ def _launch_grouped_fixed(workspace: GroupedWorkspace, cfg: KernelConfig, dtype_
         workspace.problem_count, m, n, k, 1 if workspace.homogeneous else 0,
         workspace.tile_count_for(cfg), dtype_code, precision,
         cfg.block_m, cfg.block_n, cfg.block_k, cfg.group_size_m, cfg.num_warps, cfg.num_stages,
-        _grid_size(workspace, cfg), 1 if _vector_layout(workspace, dtype_code) else 0,
+        _grid_size(workspace, cfg), 1 if vector else 0,
     )
     if schedule == "stealing":
         queue = _native.tile_queue(workspace.a[0].device, stream)

@@ -401,3 +401,18 @@ def test_tuner_skips_rejected_candidates_and_keeps_a_preferred_one_within_its_ma
     launch, _ = _fake_tuner_timing(monkeypatch, {"a": 1.0}, failing=("a",))
     with pytest.raises(RuntimeError, match="every autotune candidate failed"):
         _tune(["a"], launch)
+
+
+def test_workspace_shape_stats_follow_the_shapes_tuple():
+    """max_m/max_n/max_k and tile_count_for are cached per ``shapes`` tuple; assigning a new tuple
+    (a rebuilt routing) recomputes them."""
+    from kernels.grouped_gemm import build_grouped_workspace
+    from kernels.matmul import KernelConfig
+
+    ws = build_grouped_workspace([(8, 64, 128)] * 3, torch.bfloat16, seed=1, device="cpu")
+    cfg = KernelConfig(16, 128, 64, 8, 4, 2)
+    assert (ws.max_m, ws.max_n, ws.max_k, ws.tile_count_for(cfg)) == (8, 128, 64, 3)
+    ws.shapes = ((8, 64, 128), (40, 96, 256), (8, 64, 128))
+    assert (ws.max_m, ws.max_n, ws.max_k) == (40, 256, 96)
+    assert ws.tile_count_for(cfg) == 1 + 3 * 2 + 1
+    assert ws.tile_count_for(KernelConfig(32, 256, 64, 8, 4, 2)) == 1 + 2 + 1
