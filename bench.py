@@ -19,7 +19,8 @@
   the reference times W13 without the activation) and the headline's work under lognormal routing
   (rows around 512 and around 64 per expert) over the expert-sorted layout, timed under the static
   and the work-stealing tile schedule; each
-  is timed the same way and checked against a float32 torch reference on a sample of experts.
+  is timed the same way and checked against a float32 torch reference on a sample of experts.  The
+  DSV3 cases time K/2 steps or, for short kernels, as many as make up 10 ms (``timed_steps``).
 * ``cpu_baseline`` times the reference's own CPU torch path for the headline step on the host cores
   (per-expert ``torch.mm`` and ``F.grouped_mm`` over the padded offs layout; the faster is
   reported, with core count and CPU model); ``cpu_oracle_port`` adds the oracle's C GEMM.
@@ -129,10 +130,14 @@ def _timed(step, steps: int, warmup: int, settle_s: float = 0.0) -> tuple[float,
 
 
 def _case(projection: str, parallel_type: str, m: int, steps: int, warmup: int, seed: int = 1234,
-          pinned=None, model: str = "dsv3", settle_s: float = 0.0, b_stream=None) -> dict:
+          pinned=None, model: str = "dsv3", settle_s: float = 0.0, b_stream=None,
+          min_timed_ms: float = 0.0) -> dict:
     """Time one case of a BASELINE.json model (DSV3 by default); ``pinned`` (a KernelConfig) skips autotuning.
 
-    ``b_stream`` pins the B copy policy (None: the tuner times both; with ``pinned``, 0)."""
+    ``b_stream`` pins the B copy policy (None: the tuner times both; with ``pinned``, 0).  The settled
+    timing runs ``steps`` steps, or more when they would take under ``min_timed_ms``: the latency from
+    the start event to the first kernel (some 0.1-0.2 ms) is spread over the timed steps, which for a
+    0.2 ms kernel and 10 steps reads as 10 % slower launches."""
     import torch
 
     from kernels.grouped_gemm import launch_grouped
@@ -151,7 +156,8 @@ def _case(projection: str, parallel_type: str, m: int, steps: int, warmup: int, 
     error = _check_sample(workspace)
 
     cold_ms, _ = _timed(step, steps, warmup)  # straight after the idle check, no settle period
-    ms, wall_ms = _timed(step, steps, warmup, settle_s)
+    timed_steps = max(steps, math.ceil(min_timed_ms / cold_ms)) if cold_ms > 0 else steps
+    ms, wall_ms = _timed(step, timed_steps, warmup, settle_s)
     # Device time per launch from hipGraph replays (the reference's timing method): for kernels
     # shorter than the Python launch path the eager loop above measures the host, not the kernel.
     from utils.benchmark import time_cuda
@@ -166,6 +172,7 @@ def _case(projection: str, parallel_type: str, m: int, steps: int, warmup: int, 
         "case": f"{model}_{projection.lower()}_{parallel_type.lower()}_me{m}",
         "experts": workspace.problem_count, "shape_mkn": list(workspace.shapes[0]),
         "ms": ms, "wall_ms": wall_ms, "cold_ms": cold_ms, "graph_ms": graph_ms, "settle_s": settle_s,
+        "timed_steps": timed_steps,
         "tflops": tflops, "gbs": gbs, "bound": bound,
         "frac": tflops / PEAK_BF16_TFLOPS if bound == "mfma" else gbs / PEAK_HBM_GBS,
         "config": workspace.config.as_dict(), "scheduler": workspace.scheduler,
@@ -500,7 +507,7 @@ def main(argv=None) -> int:
                                             ("W2", "EP", 512), ("W2", "TP", 512), ("W2", "EP", 8),
                                             ("W2", "TP", 8)):
             cases.append(_progress(_case(projection, parallel_type, m, max(5, args.steps // 2), 2,
-                                         settle_s=case_settle)))
+                                         settle_s=case_settle, min_timed_ms=10.0)))
         cases.append(_progress(_swiglu_case(512, max(5, args.steps // 2), 2, settle_s=case_settle)))
         for mean_rows in (512, 64):
             cases.append(_progress(_ragged_case(max(5, args.steps // 2), 2, settle_s=case_settle, mean_rows=mean_rows)))
